@@ -1,0 +1,231 @@
+#!/usr/bin/env python3
+"""Projection-GEMM benchmark on one MI355X.
+
+One step = the whole projection stack of the model (every layer's
+projections, fused epilogues included) over one packed ragged batch whose
+inputs are already resident in HBM.  Default workload: ModernBERT-base
+shapes (22 layers, hidden 768, intermediate 1152) in bf16, sequence lengths
+U[16,512] packed to an 8192-token budget, a fresh batch (and so a fresh M)
+every step from a cycle of pre-drawn batches.  Weights N(0, 0.02) and
+activations N(0, 1), seeded, synthetic.
+
+Prints ONE JSON line.  `value` is the projection throughput in TFLOP/s
+(algorithmic 2*M*N*K per projection); tokens/s and the fraction of the bf16
+dense MFMA peak ride along.  `roofline` is the dominant kernel (largest total
+time) timed with HIP events on the stream the projections run on, in a pass
+identical to the timed one.  `cpu_baseline` is the CPU oracle's f32
+projection stack (ModernBERT-base, M = 8 x 128 = 1024) on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (published)
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E (published)
+RIDGE = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+
+WORKLOADS = {
+    # name: (stack config, length range, budget, exact packing)
+    "modernbert-base": ("modernbert-base", (16, 512), 8192, False),
+    "modernbert-large": ("modernbert-large", None, None, False),
+    "qwen35-small": ("qwen35-small", (64, 2048), 8192, True),
+    "qwen35-27b": ("qwen35-27b", (32, 1024), 4096, True),
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="modernbert-base", choices=sorted(WORKLOADS))
+    ap.add_argument("--tokens", type=int, default=None,
+                    help="fixed packed M instead of ragged draws (e.g. the large-config sweep)")
+    ap.add_argument("--batches", type=int, default=8, help="distinct ragged batches cycled")
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-roofline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The CPU oracle's f32 projection stack, ModernBERT-base shapes at
+    M = 8 x 128 = 1024 tokens (the reference's CPU configuration), run
+    layer after layer until `seconds` have passed."""
+    import numpy as np
+    from oracle import oracle as orc
+    from sys1_amd.stacks import CONFIGS
+    cfg = CONFIGS["modernbert-base"]()
+    M = 1024
+    H, I = 768, 1152
+    x = orc.fill_normal((M, H), 1)
+    ws = [orc.fill_normal((p.N, p.K), 100 + i, 0.02) for i, p in enumerate(cfg.layers[0])]
+    orc.linear_f32(x[:64], ws[0])  # load + thread start-up outside the clock
+    flops = 0
+    layers = 0
+    h = x
+    t0 = time.perf_counter()
+    while True:
+        qkv = orc.linear_f32(h, ws[0])
+        h1 = orc.linear_f32(np.ascontiguousarray(qkv[:, 2 * H:]), ws[1]) + h
+        g = orc.geglu(orc.linear_f32(h1, ws[2]))
+        h = orc.linear_f32(g, ws[3]) + h1
+        layers += 1
+        flops += sum(p.flops(M) for p in cfg.layers[0])
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or len(os.sched_getaffinity(0))
+    return {"value": round(flops / el / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"ModernBERT-base projection layers (Wqkv, Wo, Wi+GeGLU, Wo) f32 at "
+                      f"M=1024 (8x128), {layers} layers in {el:.1f} s; "
+                      f"{layers * M / el:.0f} layer-tokens/s = {layers * M / el / 22:.0f} "
+                      f"22-layer tokens/s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
+              "(the projection path runs on a single MI355X; multi-GPU sharding is a design "
+              "note only).", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from sys1_amd import batching
+    from sys1_amd.device import HipDevice
+    from sys1_amd.stacks import CONFIGS, ProjectionStack
+
+    cfg_name, lens, budget, exact = WORKLOADS[args.workload]
+    cfg = CONFIGS[cfg_name]()
+    if args.tokens:
+        Ms = [args.tokens]
+        batch_desc = f"fixed M={args.tokens}"
+    else:
+        if lens is None:
+            raise SystemExit(f"--workload {args.workload} needs --tokens")
+        Ms = [int(batching.draw_lengths(args.seed + b, lens[0], lens[1], budget, exact).sum())
+              for b in range(args.batches)]
+        batch_desc = (f"lengths U[{lens[0]},{lens[1]}] packed to {budget}"
+                      f"{' exactly' if exact else ''}, {args.batches} batches cycled")
+    max_m = max(Ms)
+
+    torch.cuda.set_device(0)
+    dev = HipDevice(0)
+    stack = ProjectionStack(cfg, dev, max_m, seed=args.seed)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(args.seed + 1000)
+    x = torch.randn(max_m, cfg.hidden, generator=gen, device="cuda:0").to(torch.bfloat16)
+    prepared = [stack.prepare(x, M) for M in Ms]
+    torch.cuda.synchronize()
+
+    for s in range(args.warmup):
+        stack.run_prepared(prepared[s % len(Ms)])
+    torch.cuda.synchronize()
+
+    # Timed region: exactly `steps` steps, synchronised on both sides.
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    start.record()
+    for s in range(args.steps):
+        stack.run_prepared(prepared[s % len(Ms)])
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms = start.elapsed_time(end)
+    tokens = sum(Ms[s % len(Ms)] for s in range(args.steps))
+    flops = tokens * cfg.flops_per_token()
+    tflops = flops / (ms * 1e-3) / 1e12
+
+    # Roofline pass: same steps, HIP events around every launch, grouped by
+    # projection kind (each kind is one kernel instantiation per shape).
+    roofline = None
+    per_proj = {}
+    if not args.no_roofline:
+        recs = []
+        for s in range(args.steps):
+            for p, a in prepared[s % len(Ms)]:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                rc = stack._fn(*a)
+                e1.record()
+                if rc:
+                    raise RuntimeError(f"launch failed: {rc}")
+                recs.append((p, a[10], e0, e1))
+        torch.cuda.synchronize()
+        for p, M, e0, e1 in recs:
+            d = per_proj.setdefault(p.name, {"n": 0, "ms": 0.0, "flop": 0, "bytes": 0,
+                                             "K": p.K, "N": p.N})
+            d["n"] += 1
+            d["ms"] += e0.elapsed_time(e1)
+            d["flop"] += p.flops(M)
+            d["bytes"] += p.bytes(M)
+        name = max(per_proj, key=lambda k: per_proj[k]["ms"])
+        d = per_proj[name]
+        avg_s = d["ms"] / d["n"] * 1e-3
+        flop_per = d["flop"] / d["n"]
+        byte_per = d["bytes"] / d["n"]
+        ai = flop_per / byte_per
+        kid, kname = dev.query_kernel(int(np.mean(Ms)), d["N"], d["K"], 0)
+        if ai >= RIDGE:
+            achieved = flop_per / avg_s / 1e12
+            roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                        "traffic": None}
+        else:
+            achieved = byte_per / avg_s / 1e9
+            roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                        "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                        "traffic": None}
+        roofline.update({"kernel": f"{name} ({kname})", "avg_us": round(avg_s * 1e6, 2),
+                         "algorithmic_per_launch": {"flop": int(flop_per), "bytes": int(byte_per)}})
+        for k, v in per_proj.items():
+            v["avg_us"] = round(v["ms"] / v["n"] * 1e3, 2)
+            v["tflops"] = round(v["flop"] / (v["ms"] * 1e-3) / 1e12, 1)
+            v["gbs"] = round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1)
+            for key in ("ms", "flop", "bytes", "n"):
+                v.pop(key)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    line = {
+        "metric": "projection TFLOP/s (% bf16 MFMA peak) + encoder tokens/s @ 8192-token batch",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) random-init weights)",
+        "config": {"workload": f"{cfg.name} projection stack: {cfg.description}; {batch_desc}",
+                   "layers": len(cfg.layers), "hidden": cfg.hidden,
+                   "packed_M": Ms, "flop_per_token": cfg.flops_per_token(),
+                   "weight_bytes": cfg.weight_bytes(), "parallelism": "single GPU"},
+        "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+        "pct_bf16_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "wall_s_timed": round(wall, 4),
+        "roofline": roofline,
+        "per_projection": per_proj,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,130 @@
+/*
+ * sys1hip -- C ABI of the MI355X (gfx950) projection-GEMM path.
+ *
+ * Drop-in for the dense projections that sys1's model code runs through
+ * `candle_nn::Linear` (weight [out,in] row-major, y = x.W^T (+ b)):
+ *   src/archs/modernbert.rs:1036-1046  linear_no_bias_dtype -> Linear::new(w, None)
+ *   src/archs/qwen35_text.rs:174-176   linear -> Linear::new(w, None)
+ *   src/models/laya.rs:620-630         linear_dtype -> Linear::new(w, Some(b))
+ * and, as fused epilogues, for the elementwise ops that follow them:
+ *   src/archs/modernbert.rs:521-533 + src/kernels/modernbert.cu:4-29  (GeGLU)
+ *   src/archs/qwen35_text.rs:232-240                                 (SwiGLU)
+ *   src/archs/modernbert.rs:883,886; src/archs/qwen35_text.rs:938-939 (residual)
+ *   src/models/laya.rs:510-520                                        (bias + gelu_erf)
+ *
+ * Conventions
+ *   - All tensors are device pointers (hipMalloc'd or torch-owned) in bf16,
+ *     row-major, leading dimensions in elements.  x is [M,K], w is [N,K],
+ *     y is [M,Nout] with Nout = N, or N/2 for the gated epilogues.
+ *   - K, ldx and ldw must be multiples of 8 elements and x, w 16-byte
+ *     aligned (128-bit loads).  y, residual and bias have no alignment rule
+ *     beyond bf16's 2 bytes (aligned runs use 64-bit stores).  M may be 0.
+ *   - The call allocates nothing and does not synchronise: work is enqueued on
+ *     the context's stream (default: the context's own stream, or the one set
+ *     by sys1hip_set_stream).
+ *   - One context per stream.  Calls on one context must not overlap: the
+ *     split-K workspace held by the context is shared by its calls.
+ *   - Return value 0 on success, a negative SYS1HIP_E* code otherwise; the
+ *     message is available from sys1hip_last_error (per calling thread).
+ *     This mirrors the reference's native-op error path, which bails with a
+ *     message on bad layout, dtype or launch size
+ *     (src/archs/modernbert.rs:553-572,610).
+ */
+#ifndef SYS1HIP_H
+#define SYS1HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SYS1HIP_API __attribute__((visibility("default")))
+
+#define SYS1HIP_OK 0
+#define SYS1HIP_EINVAL (-22)   /* bad shape, null pointer, unsupported epilogue   */
+#define SYS1HIP_EALIGN (-14)   /* pointer or leading dimension not 16-byte aligned */
+#define SYS1HIP_EDEVICE (-19)  /* no HIP device / HIP runtime error                */
+#define SYS1HIP_ERANGE (-34)   /* a size overflows what the kernels index          */
+
+/* Epilogue flags for sys1hip_linear_bf16 (bitwise OR).  Rounding follows the
+ * reference's unfused bf16 sequence: the projection is rounded to bf16 first,
+ * then each following op computes in f32 and rounds to bf16. */
+#define SYS1HIP_EPI_NONE 0
+#define SYS1HIP_EPI_BIAS 1     /* y = bf16(bf16(xW^T) + b)            candle Linear bias add */
+#define SYS1HIP_EPI_GEGLU 2    /* y = bf16(bf16(gelu_erf(g)) * u)     modernbert.cu:9-14     */
+#define SYS1HIP_EPI_SWIGLU 4   /* y = bf16(bf16(silu(g)) * u)         qwen35_text.rs:239     */
+#define SYS1HIP_EPI_RESIDUAL 8 /* y = bf16(bf16(...) + r)             modernbert.rs:883,886  */
+#define SYS1HIP_EPI_GELU 16    /* y = bf16(gelu_erf(bf16(... + b)))   laya.rs:513-515        */
+
+/* Packing granularity of gated weights: rows are interleaved in groups of
+ * this many gate rows followed by as many up rows. */
+#define SYS1HIP_GATE_GROUP 32
+
+/* Library version (major*10000 + minor*100 + patch). */
+SYS1HIP_API int sys1hip_version(void);
+
+/* Create a context on HIP device `device`: selects the device, creates a
+ * stream and the split-K workspace.  Counterpart of src/device.rs:43-65
+ * (`device::load()` -> Device::new_cuda(0)). */
+SYS1HIP_API int sys1hip_init(int device, void** ctx);
+
+/* Destroy a context (synchronises its stream first). */
+SYS1HIP_API int sys1hip_destroy(void* ctx);
+
+/* Enqueue subsequent work on `stream` (a hipStream_t; NULL is HIP's null
+ * stream).  Lets a caller share the stream of the framework that owns the
+ * buffers (e.g. torch's current stream). */
+SYS1HIP_API int sys1hip_set_stream(void* ctx, void* stream);
+
+/* Block until the context's stream is idle. */
+SYS1HIP_API int sys1hip_sync(void* ctx);
+
+/* Message of the last failing call on this thread ("" if none). */
+SYS1HIP_API const char* sys1hip_last_error(void* ctx);
+
+/* The projection: y[M,Nout] = epilogue(x[M,K] . w[N,K]^T).
+ * Replaces `Tensor::apply(&Linear)` / `Linear::forward` (candle-nn 0.11.0) at
+ * the call sites listed above.
+ *   bias      [N] (or [N/2] gated), required iff SYS1HIP_EPI_BIAS
+ *   residual  [M,Nout] with leading dim ldr, required iff SYS1HIP_EPI_RESIDUAL
+ *   GEGLU / SWIGLU require w in the packed gate/up layout written by
+ *   sys1hip_pack_gated_weight, N even and N/2 a multiple of 32. */
+SYS1HIP_API int sys1hip_linear_bf16(void* ctx,
+                        const uint16_t* x, int64_t ldx,
+                        const uint16_t* w, int64_t ldw,
+                        const uint16_t* bias,
+                        const uint16_t* residual, int64_t ldr,
+                        uint16_t* y, int64_t ldy,
+                        int64_t M, int64_t N, int64_t K,
+                        int32_t epilogue);
+
+/* Re-order a gated weight [2I, K] = [gate rows; up rows] (the reference's
+ * chunk(2) split, src/archs/modernbert.rs:531-532, or gate_proj/up_proj
+ * stacked, src/archs/qwen35_text.rs:205-231) into groups of 32 gate rows
+ * followed by the matching 32 up rows, so that one output tile holds both
+ * halves.  Load-time only (counterpart of the weight cast in
+ * linear_no_bias_dtype, src/archs/modernbert.rs:1043).  `packed` must not
+ * alias `w`.  N = 2I. */
+SYS1HIP_API int sys1hip_pack_gated_weight(void* ctx, const uint16_t* w, uint16_t* packed,
+                              int64_t N, int64_t K);
+
+/* Kernel choice for a shape (for profiling and reports): returns the kernel
+ * id the dispatcher would launch, and writes its name into `name` (up to
+ * `cap` bytes including the terminator). */
+SYS1HIP_API int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epilogue,
+                         char* name, int64_t cap);
+
+/* Force a kernel id for subsequent calls on this context (-1 = automatic
+ * choice).  Used by the tile sweep and by tests that cover every kernel. */
+SYS1HIP_API int sys1hip_set_kernel(void* ctx, int32_t kernel_id);
+
+/* Number of kernel ids and the name of one id (for sweeps). */
+SYS1HIP_API int sys1hip_kernel_count(void);
+SYS1HIP_API const char* sys1hip_kernel_name(int32_t kernel_id);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SYS1HIP_H */

@@ -1,0 +1,91 @@
+"""ctypes binding of libsys1hip.so (include/sys1hip.h).
+
+The shared library is the product: there is no Python or CPU fallback.  If
+it is missing, importing this module raises, naming the build command.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libsys1hip.so")
+
+# Epilogue flags (include/sys1hip.h).
+EPI_NONE = 0
+EPI_BIAS = 1
+EPI_GEGLU = 2
+EPI_SWIGLU = 4
+EPI_RESIDUAL = 8
+EPI_GELU = 16
+GATE_GROUP = 32
+
+OK = 0
+EINVAL = -22
+EALIGN = -14
+EDEVICE = -19
+ERANGE = -34
+
+# Every symbol the header declares; the ABI test checks the library exports them.
+EXPORTS = (
+    "sys1hip_version", "sys1hip_init", "sys1hip_destroy", "sys1hip_set_stream",
+    "sys1hip_sync", "sys1hip_last_error", "sys1hip_linear_bf16",
+    "sys1hip_pack_gated_weight", "sys1hip_query_kernel", "sys1hip_set_kernel",
+    "sys1hip_kernel_count", "sys1hip_kernel_name",
+)
+
+
+class Sys1HipError(RuntimeError):
+    """A failing sys1hip call: the return code and the library's message."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"sys1hip error {code}: {message}")
+        self.code = code
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m sys1_amd.build` "
+            "(there is no fallback path)")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+    L.sys1hip_version.restype = ctypes.c_int
+    L.sys1hip_version.argtypes = []
+    L.sys1hip_init.argtypes = [ctypes.c_int, ctypes.POINTER(vp)]
+    L.sys1hip_destroy.argtypes = [vp]
+    L.sys1hip_set_stream.argtypes = [vp, vp]
+    L.sys1hip_sync.argtypes = [vp]
+    L.sys1hip_last_error.argtypes = [vp]
+    L.sys1hip_last_error.restype = ctypes.c_char_p
+    L.sys1hip_linear_bf16.argtypes = [vp, vp, i64, vp, i64, vp, vp, i64, vp, i64, i64, i64, i64, i32]
+    L.sys1hip_pack_gated_weight.argtypes = [vp, vp, vp, i64, i64]
+    L.sys1hip_query_kernel.argtypes = [vp, i64, i64, i64, i32, ctypes.c_char_p, i64]
+    L.sys1hip_set_kernel.argtypes = [vp, i32]
+    L.sys1hip_kernel_count.argtypes = []
+    L.sys1hip_kernel_name.argtypes = [i32]
+    L.sys1hip_kernel_name.restype = ctypes.c_char_p
+    for name in ("sys1hip_init", "sys1hip_destroy", "sys1hip_set_stream", "sys1hip_sync",
+                 "sys1hip_linear_bf16", "sys1hip_pack_gated_weight", "sys1hip_query_kernel",
+                 "sys1hip_set_kernel", "sys1hip_kernel_count"):
+        getattr(L, name).restype = ctypes.c_int
+    _lib = L
+    return L
+
+
+def check(code: int, ctx=None) -> int:
+    if code < 0:
+        msg = load().sys1hip_last_error(ctx)
+        raise Sys1HipError(code, msg.decode() if msg else "")
+    return code
+
+
+def kernel_names() -> list[str]:
+    L = load()
+    return [L.sys1hip_kernel_name(i).decode() for i in range(L.sys1hip_kernel_count())]

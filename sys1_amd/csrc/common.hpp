@@ -1,0 +1,146 @@
+// Shared device helpers for the gfx950 projection kernels: vector types,
+// bf16 conversion, MFMA wrappers and the fused epilogue arithmetic.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "sys1hip.h"  // include/ is on the include path
+
+namespace sys1 {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+
+// Epilogue ids used as template arguments (a subset of flag combinations that
+// the dispatcher accepts; see epi_id_from_flags in the ABI source).
+enum Epi : int {
+  kEpiNone = 0,
+  kEpiBias = 1,
+  kEpiGeglu = 2,
+  kEpiSwiglu = 3,
+  kEpiResidual = 4,
+  kEpiBiasGelu = 5,
+  kEpiBiasResidual = 6,
+  kEpiCount = 7,
+};
+
+__host__ __device__ constexpr bool epi_gated(int e) { return e == kEpiGeglu || e == kEpiSwiglu; }
+
+// f32 -> bf16 with round-to-nearest-even (clang lowers this to the gfx950
+// hardware conversion), and back.
+__device__ __forceinline__ __bf16 to_bf16(float v) { return static_cast<__bf16>(v); }
+__device__ __forceinline__ float to_f32(__bf16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ float round_bf16(float v) { return to_f32(to_bf16(v)); }
+
+// Exact (erf) GELU: 0.5 v (1 + erf(v / sqrt 2)), the activation of the
+// reference's GeGLU (src/kernels/modernbert.cu:9-14 writes it as v * Phi(v))
+// and of candle's gelu_erf.  erff is ROCm's device-library erf.
+__device__ __forceinline__ float gelu_erf(float v) {
+  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+}
+
+// SiLU: v / (1 + e^-v) (src/archs/qwen35_text.rs:239).
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+// One output element of the non-gated epilogues from the f32 accumulator.
+// Rounding mirrors the unfused reference: projection -> bf16, then each op
+// in f32 -> bf16.
+template <int EPI>
+__device__ __forceinline__ float epi_apply(float acc, float bias, float resid) {
+  float v = round_bf16(acc);
+  if constexpr (EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual)
+    v = round_bf16(v + bias);
+  if constexpr (EPI == kEpiBiasGelu) v = round_bf16(gelu_erf(v));
+  if constexpr (EPI == kEpiResidual || EPI == kEpiBiasResidual) v = round_bf16(v + resid);
+  return v;
+}
+
+// One output element of the gated epilogues: gate and up accumulators of the
+// same output column.  GeGLU follows src/kernels/modernbert.cu:9-14 (the
+// activated gate is rounded to the storage type before the multiply);
+// SwiGLU follows candle's silu(gate) * up on bf16 tensors.
+template <int EPI>
+__device__ __forceinline__ float epi_gate(float g_acc, float u_acc) {
+  const float g = round_bf16(g_acc);
+  const float u = round_bf16(u_acc);
+  float a;
+  if constexpr (EPI == kEpiGeglu)
+    a = round_bf16(gelu_erf(g));
+  else
+    a = round_bf16(silu(g));
+  return round_bf16(a * u);
+}
+
+template <int EPI>
+__host__ __device__ constexpr bool epi_has_bias() {
+  return EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual;
+}
+template <int EPI>
+__host__ __device__ constexpr bool epi_has_resid() {
+  return EPI == kEpiResidual || EPI == kEpiBiasResidual;
+}
+
+// Arguments shared by every GEMM kernel.
+struct GemmArgs {
+  const __bf16* x;      // [M, K], ld ldx
+  const __bf16* w;      // [N, K], ld ldw (packed gate/up layout when gated)
+  const __bf16* bias;   // [Nout] or null
+  const __bf16* resid;  // [M, Nout] ld ldr or null
+  __bf16* y;            // [M, Nout] ld ldy
+  float* ws;            // split-K partials (skinny kernel only)
+  unsigned* counters;   // split-K tile arrival counters (skinny kernel only)
+  int64_t ldx, ldw, ldr, ldy;
+  int M, N, K, Nout;
+  int splits;           // split-K factor (skinny kernel only)
+};
+
+// Map the hardware workgroup id to a logical tile id so that each XCD gets a
+// contiguous range of logical tiles.  Workgroups are dispatched round-robin
+// over the 8 XCDs (id % 8); the mapping is a bijection for any count.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  constexpr int kXcds = 8;
+  const int per = nblocks / kXcds;
+  const int rem = nblocks % kXcds;
+  const int xcd = bid % kXcds;
+  const int idx = bid / kXcds;
+  return xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+}
+
+// Store 4 consecutive bf16 of one row: one 8-byte store when all 4 are in
+// range and the address is 8-byte aligned, else element by element (odd
+// output widths and leading dimensions).
+__device__ __forceinline__ bool aligned8(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 7) == 0;
+}
+
+__device__ __forceinline__ void store4(__bf16* p, const float v[4], int valid) {
+  if (valid >= 4 && aligned8(p)) {
+    bf16x4 o;
+    o[0] = to_bf16(v[0]);
+    o[1] = to_bf16(v[1]);
+    o[2] = to_bf16(v[2]);
+    o[3] = to_bf16(v[3]);
+    *reinterpret_cast<bf16x4*>(p) = o;
+  } else {
+    for (int j = 0; j < valid && j < 4; ++j) p[j] = to_bf16(v[j]);
+  }
+}
+
+__device__ __forceinline__ void load4(const __bf16* p, float v[4], int valid) {
+  if (valid >= 4 && aligned8(p)) {
+    const bf16x4 i = *reinterpret_cast<const bf16x4*>(p);
+    v[0] = to_f32(i[0]);
+    v[1] = to_f32(i[1]);
+    v[2] = to_f32(i[2]);
+    v[3] = to_f32(i[3]);
+  } else {
+    for (int j = 0; j < 4; ++j) v[j] = j < valid ? to_f32(p[j]) : 0.0f;
+  }
+}
+
+}  // namespace sys1

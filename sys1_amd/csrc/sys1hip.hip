@@ -1,0 +1,381 @@
+// C ABI of the gfx950 projection path (declared in include/sys1hip.h):
+// context/stream management, argument validation, kernel table and the
+// tile-choice heuristic keyed on the packed token count M.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "common.hpp"
+#include "gemm_skinny.hpp"
+#include "gemm_tile.hpp"
+
+using namespace sys1;
+
+namespace {
+
+constexpr int kVersion = 100;                        // 0.1.0
+constexpr size_t kWorkspaceBytes = 64ull << 20;      // split-K partials
+constexpr int kCounterSlots = 1 << 16;               // split-K arrival counters
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                     \
+  do {                                                                                    \
+    hipError_t e_ = (expr);                                                               \
+    if (e_ != hipSuccess) return fail(SYS1HIP_EDEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+struct Context {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;
+  float* ws = nullptr;
+  unsigned* counters = nullptr;
+  int forced_kernel = -1;
+  int forced_splits = 0;
+  int cus = 256;
+};
+
+using KernelFn = void (*)(GemmArgs);
+
+enum Kind { kTile = 0, kSkinny = 1 };
+
+struct KernelEntry {
+  const char* name;
+  int kind;
+  int bm, bn, threads;  // tile kernels
+  int mb16;             // skinny kernels: padded token blocks of 16
+  int occupancy;        // resident workgroups per CU (LDS/register bound)
+  float efficiency;     // relative per-CU MFMA efficiency, for the heuristic
+  KernelFn fn[kEpiCount];
+};
+
+template <int BM, int BN, int WM, int WN>
+constexpr KernelEntry tile_entry(const char* name, int occ, float eff) {
+  return KernelEntry{name, kTile, BM, BN, WM * WN * 64, 0, occ, eff,
+                     {gemm_tile_kernel<BM, BN, WM, WN, 0>, gemm_tile_kernel<BM, BN, WM, WN, 1>,
+                      gemm_tile_kernel<BM, BN, WM, WN, 2>, gemm_tile_kernel<BM, BN, WM, WN, 3>,
+                      gemm_tile_kernel<BM, BN, WM, WN, 4>, gemm_tile_kernel<BM, BN, WM, WN, 5>,
+                      gemm_tile_kernel<BM, BN, WM, WN, 6>}};
+}
+
+template <int MB16>
+constexpr KernelEntry skinny_entry(const char* name) {
+  return KernelEntry{name, kSkinny, 0, kSkinnyRows, kSkinnyThreads, MB16, 1, 1.0f,
+                     {gemm_skinny_kernel<MB16, 0>, gemm_skinny_kernel<MB16, 1>,
+                      gemm_skinny_kernel<MB16, 2>, gemm_skinny_kernel<MB16, 3>,
+                      gemm_skinny_kernel<MB16, 4>, gemm_skinny_kernel<MB16, 5>,
+                      gemm_skinny_kernel<MB16, 6>}};
+}
+
+const KernelEntry kKernels[] = {
+    tile_entry<256, 256, 2, 2>("tile_256x256_w2x2", 1, 1.00f),
+    tile_entry<256, 128, 2, 2>("tile_256x128_w2x2", 1, 0.90f),
+    tile_entry<128, 128, 2, 2>("tile_128x128_w2x2", 2, 0.80f),
+    tile_entry<128, 64, 4, 1>("tile_128x64_w4x1", 3, 0.60f),
+    tile_entry<256, 256, 2, 4>("tile_256x256_w2x4", 1, 1.00f),
+    skinny_entry<1>("skinny_m16"),
+    skinny_entry<2>("skinny_m32"),
+    skinny_entry<4>("skinny_m64"),
+    skinny_entry<8>("skinny_m128"),
+    skinny_entry<16>("skinny_m256"),
+};
+constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
+constexpr int kFirstSkinny = 5;
+constexpr int kAutoTileCandidates = 4;  // ids 0..3 take part in the automatic choice
+
+int epi_id_from_flags(int32_t f) {
+  switch (f) {
+    case SYS1HIP_EPI_NONE: return kEpiNone;
+    case SYS1HIP_EPI_BIAS: return kEpiBias;
+    case SYS1HIP_EPI_GEGLU: return kEpiGeglu;
+    case SYS1HIP_EPI_SWIGLU: return kEpiSwiglu;
+    case SYS1HIP_EPI_RESIDUAL: return kEpiResidual;
+    case SYS1HIP_EPI_BIAS | SYS1HIP_EPI_GELU: return kEpiBiasGelu;
+    case SYS1HIP_EPI_BIAS | SYS1HIP_EPI_RESIDUAL: return kEpiBiasResidual;
+    default: return -1;
+  }
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Automatic kernel choice.  M <= 256: the weight-streaming kernel sized to
+// the padded token count.  Otherwise the tile shape that minimises
+// (tile rounds over the CUs) x (tile work) / (relative efficiency).
+int choose_kernel(const Context* c, int64_t M, int64_t N, int64_t K) {
+  (void)K;
+  if (M <= 256) {
+    const int64_t blocks = cdiv(M, 16);
+    int mb = 1;
+    while (mb < blocks) mb *= 2;
+    int id = kFirstSkinny;
+    for (int b = 1; b < mb; b *= 2) ++id;
+    return id;
+  }
+  int best = 0;
+  double best_cost = 1e300;
+  for (int id = 0; id < kAutoTileCandidates; ++id) {
+    const KernelEntry& e = kKernels[id];
+    const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
+    const int64_t rounds = cdiv(tiles, (int64_t)c->cus);
+    const double cost = (double)rounds * e.bm * e.bn / e.efficiency;
+    if (cost < best_cost) best_cost = cost, best = id;
+  }
+  return best;
+}
+
+int skinny_splits(const Context* c, int mb16, int64_t N, int64_t K) {
+  const int64_t tiles = cdiv(N, kSkinnyRows);
+  const int ks = mb16 >= 16 ? 64 : 128;
+  const int64_t nslab = cdiv(K, ks);
+  int64_t s;
+  if (c->forced_splits > 0) {
+    s = c->forced_splits;
+  } else {
+    // Aim for about two workgroups per CU; keep at least 2 slabs per split.
+    s = cdiv(2 * (int64_t)c->cus, tiles);
+    s = std::min<int64_t>(s, std::max<int64_t>(1, nslab / 2));
+  }
+  s = std::max<int64_t>(1, std::min<int64_t>(s, nslab));
+  const int64_t tile_bytes = (int64_t)4 * 2 * mb16 * 64 * 16;
+  if (tiles > kCounterSlots) return 1;
+  while (s > 1 && s * tiles * tile_bytes > (int64_t)kWorkspaceBytes) --s;
+  return (int)s;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+__global__ void pack_gated_kernel(const i32x4* __restrict__ w, i32x4* __restrict__ out,
+                                  int64_t N, int64_t kv) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= N * kv) return;
+  const int64_t p = idx / kv;
+  const int64_t k = idx % kv;
+  const int64_t I = N / 2;
+  const int64_t g = p / (2 * SYS1HIP_GATE_GROUP);
+  const int64_t r = p % (2 * SYS1HIP_GATE_GROUP);
+  const int64_t src = r < SYS1HIP_GATE_GROUP ? g * SYS1HIP_GATE_GROUP + r
+                                             : I + g * SYS1HIP_GATE_GROUP + (r - SYS1HIP_GATE_GROUP);
+  out[p * kv + k] = w[src * kv + k];
+}
+
+int use_device(Context* c) {
+  int cur = -1;
+  HIP_TRY(hipGetDevice(&cur));
+  if (cur != c->device) HIP_TRY(hipSetDevice(c->device));
+  return SYS1HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sys1hip_version(void) { return kVersion; }
+
+int sys1hip_kernel_count(void) { return kNumKernels; }
+
+const char* sys1hip_kernel_name(int32_t id) {
+  return (id >= 0 && id < kNumKernels) ? kKernels[id].name : nullptr;
+}
+
+const char* sys1hip_last_error(void* ctx) {
+  (void)ctx;
+  return g_last_error.c_str();
+}
+
+int sys1hip_init(int device, void** out) {
+  if (!out) return fail(SYS1HIP_EINVAL, "sys1hip_init: null output pointer");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0)
+    return fail(SYS1HIP_EDEVICE, "sys1hip_init: no HIP device (%s)", hipGetErrorString(e));
+  if (device < 0 || device >= n)
+    return fail(SYS1HIP_EINVAL, "sys1hip_init: device %d out of range (0..%d)", device, n - 1);
+  HIP_TRY(hipSetDevice(device));
+  Context* c = new Context();
+  c->device = device;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+    c->cus = prop.multiProcessorCount;
+  if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess ||
+      hipMalloc(&c->ws, kWorkspaceBytes) != hipSuccess ||
+      hipMalloc(&c->counters, kCounterSlots * sizeof(unsigned)) != hipSuccess ||
+      hipMemsetAsync(c->counters, 0, kCounterSlots * sizeof(unsigned), c->own) != hipSuccess ||
+      hipStreamSynchronize(c->own) != hipSuccess) {
+    const char* msg = hipGetErrorString(hipGetLastError());
+    if (c->counters) (void)hipFree(c->counters);
+    if (c->ws) (void)hipFree(c->ws);
+    if (c->own) (void)hipStreamDestroy(c->own);
+    delete c;
+    return fail(SYS1HIP_EDEVICE, "sys1hip_init: device set-up failed (%s)", msg);
+  }
+  if (const char* s = getenv("SYS1HIP_SPLITS")) c->forced_splits = atoi(s);
+  c->stream = c->own;
+  *out = c;
+  return SYS1HIP_OK;
+}
+
+int sys1hip_destroy(void* ctx) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_destroy: null context");
+  Context* c = static_cast<Context*>(ctx);
+  int rc = use_device(c);
+  if (rc) return rc;
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  (void)hipFree(c->counters);
+  (void)hipFree(c->ws);
+  (void)hipStreamDestroy(c->own);
+  delete c;
+  return SYS1HIP_OK;
+}
+
+int sys1hip_set_stream(void* ctx, void* stream) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_set_stream: null context");
+  Context* c = static_cast<Context*>(ctx);
+  c->stream = static_cast<hipStream_t>(stream);
+  return SYS1HIP_OK;
+}
+
+int sys1hip_sync(void* ctx) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_sync: null context");
+  Context* c = static_cast<Context*>(ctx);
+  int rc = use_device(c);
+  if (rc) return rc;
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return SYS1HIP_OK;
+}
+
+int sys1hip_set_kernel(void* ctx, int32_t id) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_set_kernel: null context");
+  if (id < -1 || id >= kNumKernels)
+    return fail(SYS1HIP_EINVAL, "sys1hip_set_kernel: kernel id %d out of range", id);
+  static_cast<Context*>(ctx)->forced_kernel = id;
+  return SYS1HIP_OK;
+}
+
+int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epilogue, char* name,
+                         int64_t cap) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: null context");
+  if (epi_id_from_flags(epilogue) < 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: unsupported epilogue flags %d", epilogue);
+  const Context* c = static_cast<const Context*>(ctx);
+  const int id = c->forced_kernel >= 0 ? c->forced_kernel : choose_kernel(c, M, N, K);
+  if (name && cap > 0) {
+    std::string s = kKernels[id].name;
+    if (kKernels[id].kind == kSkinny)
+      s += "_s" + std::to_string(skinny_splits(c, kKernels[id].mb16, N, K));
+    snprintf(name, (size_t)cap, "%s", s.c_str());
+  }
+  return id;
+}
+
+int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t ldw,
+                        const uint16_t* bias, const uint16_t* residual, int64_t ldr, uint16_t* y,
+                        int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t epilogue) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: null context");
+  Context* c = static_cast<Context*>(ctx);
+  const int epi = epi_id_from_flags(epilogue);
+  if (epi < 0) return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: unsupported epilogue flags %d", epilogue);
+  if (M < 0 || N <= 0 || K <= 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: bad shape M=%lld N=%lld K=%lld", (long long)M,
+                (long long)N, (long long)K);
+  const bool gated = epi_gated(epi);
+  if (gated && (N % (2 * SYS1HIP_GATE_GROUP)) != 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: gated epilogue needs N %% 64 == 0 (N=%lld)",
+                (long long)N);
+  const int64_t nout = gated ? N / 2 : N;
+  if (M == 0) return SYS1HIP_OK;
+  if (!x || !w || !y) return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: null x, w or y");
+  const bool want_bias = epilogue & SYS1HIP_EPI_BIAS;
+  const bool want_res = epilogue & SYS1HIP_EPI_RESIDUAL;
+  if (want_bias != (bias != nullptr))
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: bias pointer %s but epilogue flags %d",
+                bias ? "given" : "missing", epilogue);
+  if (want_res != (residual != nullptr))
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: residual pointer %s but epilogue flags %d",
+                residual ? "given" : "missing", epilogue);
+  if (ldx < K || ldw < K || ldy < nout || (want_res && ldr < nout))
+    return fail(SYS1HIP_EINVAL,
+                "sys1hip_linear_bf16: leading dimension too small (ldx=%lld ldw=%lld ldy=%lld ldr=%lld)",
+                (long long)ldx, (long long)ldw, (long long)ldy, (long long)ldr);
+  if (K % 8 || ldx % 8 || ldw % 8)
+    return fail(SYS1HIP_EALIGN, "sys1hip_linear_bf16: K, ldx and ldw must be multiples of 8");
+  if (!aligned16(x) || !aligned16(w))
+    return fail(SYS1HIP_EALIGN, "sys1hip_linear_bf16: x and w must be 16-byte aligned");
+  if (M > (1ll << 30) || N > (1ll << 30) || K > (1ll << 30))
+    return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: dimension above 2^30");
+
+  int rc = use_device(c);
+  if (rc) return rc;
+  const int id = c->forced_kernel >= 0 ? c->forced_kernel : choose_kernel(c, M, N, K);
+  const KernelEntry& e = kKernels[id];
+
+  GemmArgs a;
+  a.x = reinterpret_cast<const __bf16*>(x);
+  a.w = reinterpret_cast<const __bf16*>(w);
+  a.bias = reinterpret_cast<const __bf16*>(bias);
+  a.resid = reinterpret_cast<const __bf16*>(residual);
+  a.y = reinterpret_cast<__bf16*>(y);
+  a.ws = c->ws;
+  a.counters = c->counters;
+  a.ldx = ldx, a.ldw = ldw, a.ldr = ldr, a.ldy = ldy;
+  a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)nout;
+  a.splits = 1;
+
+  int64_t grid;
+  if (e.kind == kSkinny) {
+    if (M > 16 * e.mb16)
+      return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: kernel %s takes M <= %d, got %lld", e.name,
+                  16 * e.mb16, (long long)M);
+    a.splits = skinny_splits(c, e.mb16, N, K);
+    grid = cdiv(N, kSkinnyRows) * a.splits;
+  } else {
+    grid = cdiv(M, e.bm) * cdiv(N, e.bn);
+  }
+  if (grid <= 0 || grid > 0x7fffffff)
+    return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: grid of %lld workgroups", (long long)grid);
+  hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)grid), dim3(e.threads), 0, c->stream, a);
+  HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+
+int sys1hip_pack_gated_weight(void* ctx, const uint16_t* w, uint16_t* packed, int64_t N, int64_t K) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_pack_gated_weight: null context");
+  if (!w || !packed) return fail(SYS1HIP_EINVAL, "sys1hip_pack_gated_weight: null pointer");
+  if (w == packed) return fail(SYS1HIP_EINVAL, "sys1hip_pack_gated_weight: packed aliases w");
+  if (N <= 0 || K <= 0 || N % (2 * SYS1HIP_GATE_GROUP))
+    return fail(SYS1HIP_EINVAL, "sys1hip_pack_gated_weight: need N %% 64 == 0 and K > 0 (N=%lld K=%lld)",
+                (long long)N, (long long)K);
+  if (K % 8) return fail(SYS1HIP_EALIGN, "sys1hip_pack_gated_weight: K must be a multiple of 8");
+  if (!aligned16(w) || !aligned16(packed))
+    return fail(SYS1HIP_EALIGN, "sys1hip_pack_gated_weight: pointers must be 16-byte aligned");
+  Context* c = static_cast<Context*>(ctx);
+  int rc = use_device(c);
+  if (rc) return rc;
+  const int64_t kv = K / 8;
+  const int64_t total = N * kv;
+  const int64_t blocks = cdiv(total, 256);
+  if (blocks > 0x7fffffff) return fail(SYS1HIP_ERANGE, "sys1hip_pack_gated_weight: too large");
+  hipLaunchKernelGGL(pack_gated_kernel, dim3((unsigned)blocks), dim3(256), 0, c->stream,
+                     reinterpret_cast<const i32x4*>(w), reinterpret_cast<i32x4*>(packed), N, kv);
+  HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,70 @@
+"""HIP device context: the counterpart of sys1's `device::load()`
+(src/device.rs:43-65), which returns the one candle Device the process uses
+(`Device::new_cuda(0)` at :49-51).  Here the device is a sys1hip context on
+one GPU; its kernels run on the torch stream that is current when a
+projection is called, so they order naturally with the torch ops that own
+the buffers.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+
+class HipDevice:
+    def __init__(self, index: int = 0):
+        L = _lib.load()
+        ctx = ctypes.c_void_p()
+        _lib.check(L.sys1hip_init(int(index), ctypes.byref(ctx)))
+        self._L = L
+        self.ctx = ctx
+        self.index = int(index)
+        self.torch_device = torch.device("cuda", self.index)
+        self._stream = None
+        self.follow_torch_stream()
+
+    def follow_torch_stream(self) -> int:
+        """Point the context at torch's current stream on this device."""
+        s = torch.cuda.current_stream(self.torch_device).cuda_stream
+        if s != self._stream:
+            _lib.check(self._L.sys1hip_set_stream(self.ctx, ctypes.c_void_p(s)), self.ctx)
+            self._stream = s
+        return s
+
+    def synchronize(self) -> None:
+        _lib.check(self._L.sys1hip_sync(self.ctx), self.ctx)
+
+    def set_kernel(self, kernel_id: int) -> None:
+        """Force one kernel id (-1: automatic choice)."""
+        _lib.check(self._L.sys1hip_set_kernel(self.ctx, int(kernel_id)), self.ctx)
+
+    def query_kernel(self, M: int, N: int, K: int, epilogue: int = 0) -> tuple[int, str]:
+        buf = ctypes.create_string_buffer(96)
+        kid = _lib.check(self._L.sys1hip_query_kernel(self.ctx, M, N, K, epilogue, buf, 96), self.ctx)
+        return kid, buf.value.decode()
+
+    def close(self) -> None:
+        if self.ctx:
+            _lib.check(self._L.sys1hip_destroy(self.ctx))
+            self.ctx = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            if self.ctx:
+                self._L.sys1hip_destroy(self.ctx)
+        except Exception:
+            pass
+
+
+_default: HipDevice | None = None
+
+
+def load(index: int = 0) -> HipDevice:
+    """The process-wide device (mirrors `device::load()`): created on first use."""
+    global _default
+    if _default is None or _default.index != index:
+        _default = HipDevice(index)
+    return _default

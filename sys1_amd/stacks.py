@@ -1,0 +1,211 @@
+"""Projection stacks of the model families the reference serves, run layer by
+layer on the gfx950 kernels -- the callers of the hot path.
+
+Each stack issues exactly the projections of one transformer layer, in the
+reference's order, with the fusions this build makes (gating in the Wi /
+gate-up epilogue, residual adds in the output projections).  Everything that
+is not a projection -- norms, attention, RoPE, the DeltaNet conv/recurrence --
+is out of scope and replaced by a fixed stand-in: the output projection reads
+a column slice of the input projection's output (the V block for ModernBERT,
+the z block for DeltaNet, the q block for gated attention).  The oracle
+chain in tests applies the same stand-in, so the comparison covers the whole
+projection chain.
+
+Layer structure followed:
+  ModernBERT  src/archs/modernbert.rs:857-887 (Layer::forward), :176-192
+              (Wqkv -> attention -> Wo), :521-533 (Wi -> GeGLU -> Wo)
+  Qwen3.5     src/archs/qwen35_text.rs:932-940 (Layer::forward), :491-629
+              (DeltaNet in_proj_qkv/z/b/a, out_proj), :312-411 (gated GQA
+              q/k/v/o), :232-240 (SwiGLU MLP)
+The DeltaNet in_proj_qkv|z|b|a and the attention q|k|v are each one GEMM over
+concatenated weights (same input, row-independent outputs).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+from .device import HipDevice
+
+
+@dataclass(frozen=True)
+class Proj:
+    """One projection: y = epi(x . W^T), W [N, K]."""
+    name: str
+    K: int
+    N: int          # weight rows (2I for gated)
+    epi: int
+    src: str        # input buffer name
+    src_off: int    # first input column
+    dst: str        # output buffer name
+    resid: str | None = None
+
+    @property
+    def nout(self) -> int:
+        return self.N // 2 if self.epi in (_lib.EPI_GEGLU, _lib.EPI_SWIGLU) else self.N
+
+    def flops(self, M: int) -> int:
+        return 2 * M * self.N * self.K
+
+    def bytes(self, M: int) -> int:
+        """Algorithmic HBM bytes: read x and W once, write y, read residual."""
+        b = 2 * (M * self.K + self.N * self.K + M * self.nout)
+        if self.resid:
+            b += 2 * M * self.nout
+        return b
+
+
+@dataclass
+class StackConfig:
+    name: str
+    hidden: int
+    layers: list[list[Proj]] = field(default_factory=list)
+    description: str = ""
+
+    def flops_per_token(self) -> int:
+        return sum(p.flops(1) for layer in self.layers for p in layer)
+
+    def weight_bytes(self) -> int:
+        return sum(2 * p.N * p.K for layer in self.layers for p in layer)
+
+
+def modernbert(hidden: int, intermediate: int, layers: int, name: str) -> StackConfig:
+    H, I = hidden, intermediate
+    layer = [
+        Proj("Wqkv", H, 3 * H, _lib.EPI_NONE, "h", 0, "qkv"),
+        Proj("attn.Wo", H, H, _lib.EPI_RESIDUAL, "qkv", 2 * H, "h", resid="h"),
+        Proj("Wi+geglu", H, 2 * I, _lib.EPI_GEGLU, "h", 0, "act"),
+        Proj("mlp.Wo", I, H, _lib.EPI_RESIDUAL, "act", 0, "h", resid="h"),
+    ]
+    return StackConfig(name, H, [list(layer) for _ in range(layers)],
+                       f"ModernBERT H={H} I={I} x{layers}: Wqkv {H}->{3 * H}, Wo {H}->{H}, "
+                       f"Wi {H}->2x{I} (GeGLU), Wo {I}->{H}")
+
+
+def qwen35(hidden: int, layers: int, heads: int, kv_heads: int, head_dim: int,
+           intermediate: int, dn_qk: int, dn_v: int, dn_heads: int, o_in: int,
+           name: str) -> StackConfig:
+    """Hybrid decoder: every 4th layer gated GQA attention, the rest DeltaNet
+    (3:1).  o_in is the o_proj input width (BASELINE states heads*hd*2 for the
+    small config where the reference builds heads*hd; src/archs/qwen35_text.rs:281-285)."""
+    H = hidden
+    mlp = [
+        Proj("gate_up+swiglu", H, 2 * intermediate, _lib.EPI_SWIGLU, "h", 0, "act"),
+        Proj("down", intermediate, H, _lib.EPI_RESIDUAL, "act", 0, "h", resid="h"),
+    ]
+    dn_in = 2 * dn_qk + 2 * dn_v + 2 * dn_heads  # qkv | z | b | a
+    deltanet = [
+        Proj("in_proj_qkvzba", H, dn_in, _lib.EPI_NONE, "h", 0, "mix"),
+        Proj("out_proj", dn_v, H, _lib.EPI_RESIDUAL, "mix", 2 * dn_qk + dn_v, "h", resid="h"),
+    ] + mlp
+    q_w = 2 * heads * head_dim
+    attn_in = q_w + 2 * kv_heads * head_dim
+    attention = [
+        Proj("q_k_v", H, attn_in, _lib.EPI_NONE, "h", 0, "mix"),
+        Proj("o_proj", o_in, H, _lib.EPI_RESIDUAL, "mix", 0, "h", resid="h"),
+    ] + mlp
+    stack = [list(attention if (i + 1) % 4 == 0 else deltanet) for i in range(layers)]
+    return StackConfig(name, H, stack,
+                       f"Qwen3.5 hybrid H={H} x{layers} (3:1 DeltaNet:GQA), in_proj {H}->{dn_in}, "
+                       f"out {dn_v}->{H}, qkv {H}->{attn_in}, o {o_in}->{H}, "
+                       f"SwiGLU {H}->2x{intermediate}, down {intermediate}->{H}")
+
+
+CONFIGS = {
+    "modernbert-base": lambda: modernbert(768, 1152, 22, "modernbert-base"),
+    "modernbert-large": lambda: modernbert(1024, 2624, 28, "modernbert-large"),
+    "qwen35-small": lambda: qwen35(2048, 24, 16, 2, 128, 6144, 2048, 4096, 16, 4096,
+                                   "qwen35-small"),
+    "qwen35-27b": lambda: qwen35(5120, 64, 24, 4, 256, 17408, 2048, 6144, 48, 6144,
+                                 "qwen35-27b"),
+}
+
+
+class ProjectionStack:
+    """Weights and activation buffers of a stack on one GPU, and the layer
+    loop that enqueues its projections."""
+
+    def __init__(self, cfg: StackConfig, dev: HipDevice, max_tokens: int, seed: int = 0,
+                 weights: list[list[torch.Tensor]] | None = None, w_std: float = 0.02):
+        self.cfg = cfg
+        self.dev = dev
+        self.max_tokens = max_tokens
+        d = dev.torch_device
+        g = torch.Generator(device=d)
+        g.manual_seed(seed)
+        from .linear import pack_gated_weight
+        self.weights: list[list[torch.Tensor]] = []
+        for li, layer in enumerate(cfg.layers):
+            ws = []
+            for pi, p in enumerate(layer):
+                if weights is not None:
+                    w = weights[li][pi].to(device=d, dtype=torch.bfloat16).contiguous()
+                else:
+                    w = (torch.randn(p.N, p.K, generator=g, device=d, dtype=torch.float32) * w_std
+                         ).to(torch.bfloat16)
+                if p.epi in (_lib.EPI_GEGLU, _lib.EPI_SWIGLU):
+                    w = pack_gated_weight(w, dev)
+                ws.append(w)
+            self.weights.append(ws)
+        widths: dict[str, int] = {"h": cfg.hidden}
+        for layer in cfg.layers:
+            for p in layer:
+                widths[p.dst] = max(widths.get(p.dst, 0), p.nout)
+        # Widths rounded up to 8 elements so every row stays 16-byte aligned.
+        self.buffers = {k: torch.zeros(max_tokens, (v + 7) // 8 * 8, dtype=torch.bfloat16, device=d)
+                        for k, v in widths.items()}
+        self._fn = dev._L.sys1hip_linear_bf16
+
+    def _calls(self, x: torch.Tensor, M: int) -> list[tuple]:
+        """Argument tuples of every launch for M tokens (prepared once per M,
+        so the enqueue loop is a plain sequence of C calls)."""
+        assert x.shape[1] == self.cfg.hidden and x.dtype == torch.bfloat16 and x.stride(1) == 1
+        if M > self.max_tokens:
+            raise ValueError(f"M={M} exceeds the stack's max_tokens={self.max_tokens}")
+        bufs = self.buffers
+        calls = []
+        first_resid = True
+        for li, layer in enumerate(self.cfg.layers):
+            for pi, p in enumerate(layer):
+                if p.src == "h" and li == 0 and pi == 0:
+                    src, ldx = x.data_ptr(), x.stride(0)
+                elif p.src == "h" and first_resid:
+                    src, ldx = x.data_ptr(), x.stride(0)
+                else:
+                    b = bufs[p.src]
+                    src, ldx = b.data_ptr() + 2 * p.src_off, b.stride(0)
+                dst = bufs[p.dst]
+                rptr, ldr = None, 0
+                if p.resid:
+                    # The first residual reads the input x; later ones run in place on h.
+                    if first_resid:
+                        rptr, ldr = x.data_ptr(), x.stride(0)
+                        first_resid = False
+                    else:
+                        rptr, ldr = bufs["h"].data_ptr(), bufs["h"].stride(0)
+                w = self.weights[li][pi]
+                calls.append((p, (src, ldx, w.data_ptr(), w.stride(0), None, rptr, ldr,
+                                  dst.data_ptr(), dst.stride(0), M, p.N, p.K, p.epi)))
+        return calls
+
+    def prepare(self, x: torch.Tensor, M: int):
+        ctx = self.dev.ctx
+        return [(p, (ctx, *[ctypes.c_void_p(a) if i in (0, 2, 4, 5, 7) and a is not None else a
+                            for i, a in enumerate(args)])) for p, args in self._calls(x, M)]
+
+    def run_prepared(self, prepared) -> None:
+        fn = self._fn
+        for _, args in prepared:
+            rc = fn(*args)
+            if rc:
+                _lib.check(rc, self.dev.ctx)
+
+    def forward(self, x: torch.Tensor, M: int) -> torch.Tensor:
+        """Enqueue the whole stack for the first M rows of x; returns the
+        hidden-state buffer (first M rows valid once the stream reaches it)."""
+        self.dev.follow_torch_stream()
+        self.run_prepared(self.prepare(x, M))
+        return self.buffers["h"][:M, :self.cfg.hidden]

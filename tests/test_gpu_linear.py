@@ -1,0 +1,201 @@
+"""GPU parity of the projection kernels against the CPU oracle, through the
+C ABI (libsys1hip.so via sys1_amd.linear).
+
+Bar (per projection output): relative Frobenius error <= 1e-2 and max-abs
+error <= 2e-2 * max|ref| against the oracle's f32 projection of the reference
+f32 inputs, and -- stronger, on the same bf16 inputs -- every element within
+one bf16 ulp of the correctly rounded float64 result.
+"""
+import numpy as np
+import pytest
+
+from gpu_helpers import assert_parity, bf16_ulp, to_gpu_bf16, to_np
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from sys1_amd.device import HipDevice
+    d = HipDevice(0)
+    yield d
+    d.set_kernel(-1)
+
+
+def _inputs(orc, M, N, K, seed):
+    x = orc.fill_normal((M, K), seed)
+    w = orc.fill_normal((N, K), seed + 1, 0.02)
+    return x, w
+
+
+def _check_close_to_rounded(orc, out, ref64, what):
+    """Every element within 1 bf16 ulp (+tiny abs) of bf16(ref64)."""
+    r = orc.round_bf16(ref64.astype(np.float32))
+    err = np.abs(out.astype(np.float64) - r)
+    tol = bf16_ulp(r) + 1e-6
+    bad = err > tol
+    assert not bad.any(), f"{what}: {bad.sum()} elements off by >1 ulp, worst {err.max():.3e}"
+    return float((err == 0).mean())
+
+
+SHAPES = [
+    (1, 64, 64), (15, 48, 136), (64, 768, 768), (100, 1000, 200), (256, 2304, 768),
+    (257, 768, 1152), (300, 130, 64), (1024, 768, 768), (1024, 2304, 768), (777, 520, 328),
+]
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_linear_auto_kernel_matches_oracle(dev, orc, M, N, K):
+    from sys1_amd.linear import Linear
+    print(f"[gpu] linear auto M={M} N={N} K={K} kernel={dev.query_kernel(M, N, K)[1]}", flush=True)
+    x, w = _inputs(orc, M, N, K, 100 + M)
+    lin = Linear(to_gpu_bf16(w, torch), device=dev)
+    y = to_np(lin(to_gpu_bf16(x, torch)))
+    # The reference f32 path on the f32 inputs (the stated tolerance).
+    assert_parity(y, orc.linear_f32(x, w), f"M={M} N={N} K={K} vs f32 oracle")
+    # The same bf16 inputs: within one bf16 ulp of the exact product.
+    xb, wb = orc.round_bf16(x), orc.round_bf16(w)
+    exact = _check_close_to_rounded(orc, y, orc.linear_f64(xb, wb), f"M={M} N={N} K={K}")
+    assert exact > 0.9
+
+
+def _kernel_ids():
+    from sys1_amd import kernel_names
+    return list(enumerate(kernel_names()))
+
+
+@pytest.mark.parametrize("kid,name", _kernel_ids())
+def test_every_kernel_every_epilogue(dev, orc, kid, name):
+    """Force each kernel id and check every epilogue on ragged shapes."""
+    from sys1_amd import _lib
+    from sys1_amd.linear import GatedLinear, Linear
+    if name.startswith("skinny_"):
+        cap = int(name.split("_m")[1])
+        Ms = sorted({max(1, cap // 2 + 3), cap})
+    else:
+        Ms = [300, 513]
+    dev.set_kernel(kid)
+    try:
+        for M in Ms:
+            N, K = 384, 328
+            print(f"[gpu] kernel={name} M={M} N={N} K={K}", flush=True)
+            x, w = _inputs(orc, M, N, K, 7 + M)
+            xb, wb = orc.round_bf16(x), orc.round_bf16(w)
+            xg, wg = to_gpu_bf16(x, torch), to_gpu_bf16(w, torch)
+            proj = orc.linear_f64(xb, wb).astype(np.float32)
+            p16 = orc.round_bf16(proj)
+            bias = orc.fill_normal((N,), 3)
+            bb = orc.round_bf16(bias)
+            res = orc.fill_normal((M, N), 4)
+            rb = orc.round_bf16(res)
+            # none
+            y = to_np(Linear(wg, device=dev)(xg))
+            _check_close_to_rounded(orc, y, proj, f"{name} none")
+            # bias: bf16(bf16(p) + b)
+            y = to_np(Linear(wg, to_gpu_bf16(bias, torch), device=dev)(xg))
+            assert_parity(y, orc.round_bf16(p16 + bb), f"{name} bias")
+            assert np.abs(y - orc.round_bf16(p16 + bb)).max() <= 2 * bf16_ulp(np.abs(p16 + bb).max())
+            # residual
+            y = to_np(Linear(wg, device=dev)(xg, residual=to_gpu_bf16(res, torch)))
+            ref = orc.round_bf16(p16 + rb)
+            assert_parity(y, ref, f"{name} residual")
+            assert np.abs(y - ref).max() <= 2 * bf16_ulp(np.abs(ref).max())
+            # bias + residual
+            y = to_np(Linear(wg, to_gpu_bf16(bias, torch), device=dev)(xg, residual=to_gpu_bf16(res, torch)))
+            assert_parity(y, orc.round_bf16(orc.round_bf16(p16 + bb) + rb), f"{name} bias+residual")
+            # bias + gelu (Laya scorer_in)
+            y = to_np(Linear(wg, to_gpu_bf16(bias, torch), device=dev)(xg, gelu=True))
+            assert_parity(y, orc.round_bf16(orc.gelu_erf(orc.round_bf16(p16 + bb))), f"{name} bias+gelu")
+            # gated: GeGLU and SwiGLU over [2I, K] = [gate; up], I = N/2
+            I = N // 2
+            g16, u16 = p16[:, :I], p16[:, I:]
+            ref_geglu = orc.round_bf16(orc.round_bf16(orc.gelu_erf(g16)) * u16)
+            ref_swiglu = orc.round_bf16(orc.round_bf16(orc.silu(g16)) * u16)
+            y = to_np(GatedLinear(wg, "gelu", device=dev)(xg))
+            assert y.shape == (M, I)
+            assert_parity(y, ref_geglu, f"{name} geglu")
+            # unfused f32 reference (src/archs/modernbert.rs:531-532 on f32 tensors)
+            assert_parity(y, orc.geglu(orc.linear_f32(x, w)), f"{name} geglu vs f32")
+            y = to_np(GatedLinear(wg, "silu", device=dev)(xg))
+            assert_parity(y, ref_swiglu, f"{name} swiglu")
+            assert_parity(y, orc.swiglu(*np.split(orc.linear_f32(x, w), 2, axis=1)), f"{name} swiglu vs f32")
+    finally:
+        dev.set_kernel(-1)
+
+
+def test_strided_input_and_output(dev, orc):
+    """x as a column slice of a wider buffer (the V block of a qkv output) and
+    y written into a slice of a wider buffer."""
+    from sys1_amd.linear import Linear
+    M, H = 200, 256
+    qkv = orc.fill_normal((M, 3 * H), 21)
+    w = orc.fill_normal((H, H), 22, 0.02)
+    qkv_g = to_gpu_bf16(qkv, torch)
+    out = torch.zeros(M, 2 * H, dtype=torch.bfloat16, device="cuda:0")
+    Linear(to_gpu_bf16(w, torch), device=dev).forward_into(qkv_g[:, 2 * H:], out[:, H:])
+    y = to_np(out)
+    assert (y[:, :H] == 0).all()
+    assert_parity(y[:, H:], orc.linear_f32(qkv[:, 2 * H:], w), "strided")
+
+
+def test_leading_dims_flatten_and_empty(dev, orc):
+    from sys1_amd.linear import Linear
+    w = to_gpu_bf16(orc.fill_normal((64, 32), 1, 0.02), torch)
+    lin = Linear(w, device=dev)
+    x = orc.fill_normal((2, 5, 32), 2)
+    y = lin(to_gpu_bf16(x, torch))
+    assert y.shape == (2, 5, 64)
+    assert_parity(to_np(y).reshape(10, 64), orc.linear_f32(x.reshape(10, 32), orc.round_bf16(orc.fill_normal((64, 32), 1, 0.02))), "3d")
+    e = lin(torch.empty(0, 32, dtype=torch.bfloat16, device="cuda:0"))
+    assert e.shape == (0, 64)
+
+
+def test_tiny_output_width(dev, orc):
+    """N = 1 (the Laya scorer's last projection, src/models/laya.rs:516) with bias."""
+    from sys1_amd.linear import Linear
+    M, K = 37, 768
+    x = orc.fill_normal((M, K), 5)
+    w = orc.fill_normal((1, K), 6, 0.02)
+    b = orc.fill_normal((1,), 7)
+    y = to_np(Linear(to_gpu_bf16(w, torch), to_gpu_bf16(b, torch), device=dev)(to_gpu_bf16(x, torch)))
+    assert y.shape == (M, 1)
+    assert_parity(y, orc.linear_f32(x, w, b), "N=1")
+
+
+def test_split_k_is_deterministic_and_rearms(dev, orc):
+    """Split-K partial sums are reduced in split order: repeated calls are
+    bit-identical, and the tile counters re-arm between calls of different
+    shapes."""
+    from sys1_amd.linear import Linear
+    outs = []
+    for (M, N, K) in [(64, 1024, 4096), (32, 768, 2048), (64, 1024, 4096), (200, 4096, 2048)]:
+        _, name = dev.query_kernel(M, N, K)
+        print(f"[gpu] split-k M={M} N={N} K={K} {name}", flush=True)
+        x, w = _inputs(orc, M, N, K, 50 + M + N)
+        y = to_np(Linear(to_gpu_bf16(w, torch), device=dev)(to_gpu_bf16(x, torch)))
+        assert_parity(y, orc.linear_f32(x, w), f"split-k {M}x{N}x{K}")
+        outs.append(y)
+    np.testing.assert_array_equal(outs[0], outs[2])
+
+
+def test_python_errors(dev, orc):
+    from sys1_amd import Sys1HipError
+    from sys1_amd.linear import GatedLinear, Linear
+    w = torch.zeros(64, 64, dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(ValueError):
+        Linear(w.float(), device=dev)
+    lin = Linear(w, device=dev)
+    with pytest.raises(ValueError):
+        lin(torch.zeros(4, 32, dtype=torch.bfloat16, device="cuda:0"))
+    with pytest.raises(ValueError):
+        lin(torch.zeros(4, 64, dtype=torch.float32, device="cuda:0"))
+    big = torch.zeros(4, 72, dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(Sys1HipError) as e:
+        lin(big[:, 1:65])  # 2-byte offset: misaligned rows
+    assert e.value.code == -14
+    with pytest.raises(ValueError):
+        GatedLinear(torch.zeros(96, 64, dtype=torch.bfloat16, device="cuda:0"), device=dev)

@@ -1,0 +1,217 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each oracle function is checked against something other than its own
+formula: a library routine (numpy float64 matmul, scipy's normal CDF /
+logistic, torch's bf16 cast and layer_norm), brute force on tiny inputs,
+closed forms and invariants chosen so that a dropped term, a swapped half or
+a transposed operand fails.  Where the reference's own tests hold vectors for
+this path, they are used (GeGLU: src/archs/modernbert.rs:746-757; SwiGLU
+generator: src/archs/qwen35_text.rs:1097-1104).
+"""
+import itertools
+import math
+
+import numpy as np
+import pytest
+import scipy.special
+import scipy.stats
+
+
+def _rel_fro(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / max(np.linalg.norm(b), 1e-30))
+
+
+# ------------------------------------------------------------------ GEMM ---
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 8), (3, 5, 7), (17, 48, 64), (64, 300, 776),
+                                   (333, 129, 1000), (130, 67, 257)])
+def test_linear_f32_matches_numpy_f64(orc, M, N, K):
+    x = orc.fill_normal((M, K), 11 + M)
+    w = orc.fill_normal((N, K), 13 + N, 0.02)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    y = orc.linear_f32(x, w)
+    assert y.shape == (M, N) and y.dtype == np.float32
+    assert _rel_fro(y, ref) < 1e-6
+    y64 = orc.linear_f64(x, w)
+    assert np.abs(y64 - ref).max() <= 1e-12 * max(1.0, np.abs(ref).max()) * K
+
+
+def test_linear_brute_force_tiny(orc):
+    x = np.array([[1.0, 2.0, -3.0], [0.5, 0.0, 4.0]], np.float32)
+    w = np.array([[1.0, 0.0, 0.0], [0.0, 1.0, 0.0], [0.0, 0.0, 1.0], [1.0, -1.0, 2.0]], np.float32)
+    b = np.array([0.0, 1.0, -1.0, 0.5], np.float32)
+    expect = [[sum(x[m][k] * w[n][k] for k in range(3)) + b[n] for n in range(4)] for m in range(2)]
+    np.testing.assert_allclose(orc.linear_f32(x, w, b), expect, rtol=0, atol=1e-6)
+    np.testing.assert_allclose(orc.linear_f64(x, w, b), expect, rtol=0, atol=1e-12)
+
+
+def test_linear_weight_is_out_by_in(orc):
+    """Weight [out, in]: a non-square identity-like weight must select input
+    columns (a transposed operand would fail the shape or the values)."""
+    x = orc.fill_normal((9, 16), 3)
+    w = np.zeros((4, 16), np.float32)
+    for n, k in enumerate((0, 5, 7, 15)):
+        w[n, k] = 1.0
+    np.testing.assert_array_equal(orc.linear_f32(x, w), x[:, [0, 5, 7, 15]])
+
+
+def test_linear_closed_forms_and_invariants(orc):
+    M, N, K = 40, 24, 96
+    x = orc.fill_normal((M, K), 5)
+    w = orc.fill_normal((N, K), 6, 0.05)
+    # Rank one: x = u v^T -> y = u (W v)^T.
+    u = orc.fill_normal((M, 1), 7)
+    v = orc.fill_normal((1, K), 8)
+    y = orc.linear_f32(u @ v, w)
+    np.testing.assert_allclose(y, u @ (w @ v.T).T, rtol=1e-4, atol=1e-5)
+    # Linearity in x.
+    x2 = orc.fill_normal((M, K), 9)
+    np.testing.assert_allclose(orc.linear_f32(2 * x - x2, w),
+                               2 * orc.linear_f32(x, w) - orc.linear_f32(x2, w), rtol=1e-4, atol=1e-5)
+    # Row independence: permuting tokens permutes outputs exactly.
+    perm = np.random.default_rng(0).permutation(M)
+    np.testing.assert_array_equal(orc.linear_f32(x[perm], w), orc.linear_f32(x, w)[perm])
+    # K-split additivity.
+    y_split = orc.linear_f32(x[:, :40], w[:, :40]) + orc.linear_f32(x[:, 40:], w[:, 40:])
+    np.testing.assert_allclose(y_split, orc.linear_f32(x, w), rtol=1e-5, atol=1e-5)
+    # Bias adds per output feature.
+    b = orc.fill_normal((N,), 10)
+    np.testing.assert_allclose(orc.linear_f32(x, w, b), orc.linear_f32(x, w) + b, rtol=0, atol=1e-6)
+
+
+def test_linear_flattens_leading_dims(orc):
+    x = orc.fill_normal((2, 3, 32), 1)
+    w = orc.fill_normal((8, 32), 2)
+    y = orc.linear_f32(x, w)
+    assert y.shape == (2, 3, 8)
+    np.testing.assert_array_equal(y.reshape(6, 8), orc.linear_f32(x.reshape(6, 32), w))
+
+
+# ----------------------------------------------------------- activations ---
+
+# The 16 values of the reference's fused GeGLU test (src/archs/modernbert.rs:746-757).
+GEGLU_VALUES = [-4.0, -1.5, -0.25, 0.0, 0.5, 1.25, 3.0, 5.0, 2.0, -0.75, 0.125, -3.5, 1.0, 0.5,
+                -2.0, 4.5]
+
+
+def test_gelu_erf_against_normal_cdf(orc):
+    v = np.linspace(-8, 8, 4001).astype(np.float32)
+    expect = v.astype(np.float64) * scipy.stats.norm.cdf(v.astype(np.float64))
+    np.testing.assert_allclose(orc.gelu_erf(v), expect, rtol=2e-7, atol=1e-7)
+    # Special values and the odd-part identity gelu(v) - gelu(-v) = v.
+    assert orc.lib().orc_gelu_erf(0.0) == 0.0
+    assert abs(orc.lib().orc_gelu_erf(1.0) - 0.8413447460685429) < 1e-7
+    g = orc.gelu_erf(v) - orc.gelu_erf(-v)
+    np.testing.assert_allclose(g, v, rtol=1e-6, atol=1e-6)
+
+
+def test_geglu_reference_vector(orc):
+    """Reference input [2, 8] -> [2, 4]; first half is the gated (gelu) half."""
+    inp = np.array(GEGLU_VALUES, np.float32).reshape(2, 8)
+    out = orc.geglu(inp)
+    a, b = inp[:, :4].astype(np.float64), inp[:, 4:].astype(np.float64)
+    expect = a * scipy.stats.norm.cdf(a) * b
+    assert out.shape == (2, 4)
+    # f32 tolerance of the reference test (src/archs/modernbert.rs:758).
+    assert np.abs(out - expect).max() <= 1e-5
+    swapped = b * scipy.stats.norm.cdf(b) * a
+    assert np.abs(out - swapped).max() > 1e-2
+
+
+def test_silu_and_swiglu_reference_generator(orc):
+    """Generator of src/archs/qwen35_text.rs:1097-1104: g = ((i*97 % 1601) - 800)/73,
+    up = -0.5 g + 0.25, over [7, 4096]."""
+    i = np.arange(4096 * 7)
+    g = (((i * 97) % 1601).astype(np.float32) - 800.0) / 73.0
+    g = g.reshape(7, 4096)
+    up = (-0.5 * g + 0.25).astype(np.float32)
+    out = orc.swiglu(g, up)
+    g64 = g.astype(np.float64)
+    expect = g64 * scipy.special.expit(g64) * up.astype(np.float64)
+    assert np.abs(out - expect).max() <= 1e-5
+    s = orc.silu(g) - orc.silu(-g)  # silu(v) - silu(-v) = v
+    np.testing.assert_allclose(s, g, rtol=1e-6, atol=1e-5)
+
+
+def test_layer_norm_against_torch(orc):
+    torch = pytest.importorskip("torch")
+    x = orc.fill_normal((13, 768), 4) * 3 + 1
+    g = orc.fill_normal((768,), 5)
+    b = orc.fill_normal((768,), 6)
+    expect = torch.nn.functional.layer_norm(torch.from_numpy(x).double(), (768,),
+                                            torch.from_numpy(g).double(),
+                                            torch.from_numpy(b).double(), 1e-5).numpy()
+    np.testing.assert_allclose(orc.layer_norm(x, g, b, 1e-5), expect, rtol=1e-5, atol=1e-5)
+
+
+def test_argmax_ties_take_lowest_index(orc):
+    """src/models/laya.rs:909-916 keeps the lowest index among equal maxima."""
+    assert orc.argmax([1.0, 3.0, 3.0, 2.0]) == 1
+    assert orc.argmax([5.0]) == 0
+    assert orc.argmax([-1.0, -1.0]) == 0
+    assert orc.argmax([0.0, 1.0, 2.0, 7.0]) == 3
+
+
+# --------------------------------------------------------------- bf16 ----
+
+def test_round_bf16_round_to_nearest_even(orc):
+    cases = {1.0: 1.0, 1.0 + 2 ** -8: 1.0, 1.0 + 3 * 2 ** -8: 1.0 + 2 ** -6,
+             1.0 + 2 ** -8 + 2 ** -20: 1.0 + 2 ** -7, -2.5: -2.5, 0.0: 0.0}
+    for v, r in cases.items():
+        assert orc.lib().orc_round_bf16(v) == np.float32(r), v
+    torch = pytest.importorskip("torch")
+    x = orc.fill_normal((1 << 16,), 77) * 1000
+    expect = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(orc.round_bf16(x), expect)
+    bits = orc.to_bf16_bits(x)
+    np.testing.assert_array_equal(orc.from_bf16_bits(bits), expect)
+
+
+# --------------------------------------------------------- seeded data ---
+
+def test_fill_normal_distribution_and_reproducibility(orc):
+    a = orc.fill_normal((200_000,), 1234)
+    assert abs(a.mean()) < 0.01 and abs(a.std() - 1.0) < 0.01
+    assert scipy.stats.kstest(a[:20000], "norm").pvalue > 1e-3
+    b = orc.fill_normal((1000,), 1234)
+    np.testing.assert_array_equal(a[:1000], b)  # element i depends only on (seed, i)
+    w = orc.fill_normal((50_000,), 99, 0.02)
+    assert abs(w.std() - 0.02) < 0.0005
+    assert not np.array_equal(orc.fill_normal((10,), 1), orc.fill_normal((10,), 2))
+
+
+@pytest.mark.parametrize("seed", [0, 1, 7, 12345])
+def test_pack_ragged_contract(orc, seed):
+    lengths = orc.pack_ragged(seed, 16, 512, 8192)
+    assert lengths.sum() <= 8192 and ((lengths >= 16) & (lengths <= 512)).all()
+    # The next draw would overflow the budget (SplitMix64 element len(lengths)).
+    from sys1_amd.batching import splitmix64
+    nxt = 16 + int(splitmix64(seed, np.array([len(lengths)]))[0] % np.uint64(497))
+    assert lengths.sum() + nxt > 8192 or lengths.sum() == 8192
+    exact = orc.pack_ragged(seed, 64, 2048, 8192, exact=True)
+    assert exact.sum() == 8192 and (exact[:-1] >= 64).all()
+
+
+# ------------------------------------------------------------- golden ----
+
+def test_oracle_matches_golden_fixtures(orc):
+    """Fixtures written by tests/golden/make_golden.py from numpy/scipy
+    (independent of the oracle)."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(__file__), "golden", "projection_golden.json")
+    with open(path) as f:
+        gold = json.load(f)
+    for case in gold["linear"]:
+        x = np.array(case["x"], np.float32)
+        w = np.array(case["w"], np.float32)
+        b = np.array(case["bias"], np.float32) if case["bias"] is not None else None
+        np.testing.assert_allclose(orc.linear_f64(x, w, b), case["y"], rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(orc.linear_f32(x, w, b), case["y"], rtol=1e-5, atol=1e-5)
+    g = gold["geglu"]
+    np.testing.assert_allclose(orc.geglu(np.array(g["input"], np.float32)), g["output"], atol=1e-6)
+    s = gold["swiglu"]
+    np.testing.assert_allclose(orc.swiglu(np.array(s["gate"], np.float32), np.array(s["up"], np.float32)),
+                               s["output"], atol=1e-5, rtol=1e-6)
+    r = gold["bf16"]
+    np.testing.assert_array_equal(orc.to_bf16_bits(np.array(r["input"], np.float32)), r["bits"])
