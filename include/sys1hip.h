@@ -59,7 +59,7 @@ extern "C" {
 
 /* Packing granularity of gated weights: rows are interleaved in groups of
  * this many gate rows followed by as many up rows. */
-#define SYS1HIP_GATE_GROUP 32
+#define SYS1HIP_GATE_GROUP 16
 
 /* Library version (major*10000 + minor*100 + patch). */
 SYS1HIP_API int sys1hip_version(void);
@@ -89,7 +89,7 @@ SYS1HIP_API const char* sys1hip_last_error(void* ctx);
  *   bias      [N] (or [N/2] gated), required iff SYS1HIP_EPI_BIAS
  *   residual  [M,Nout] with leading dim ldr, required iff SYS1HIP_EPI_RESIDUAL
  *   GEGLU / SWIGLU require w in the packed gate/up layout written by
- *   sys1hip_pack_gated_weight, N even and N/2 a multiple of 32. */
+ *   sys1hip_pack_gated_weight, N even and N/2 a multiple of 16. */
 SYS1HIP_API int sys1hip_linear_bf16(void* ctx,
                         const uint16_t* x, int64_t ldx,
                         const uint16_t* w, int64_t ldw,
@@ -101,11 +101,11 @@ SYS1HIP_API int sys1hip_linear_bf16(void* ctx,
 
 /* Re-order a gated weight [2I, K] = [gate rows; up rows] (the reference's
  * chunk(2) split, src/archs/modernbert.rs:531-532, or gate_proj/up_proj
- * stacked, src/archs/qwen35_text.rs:205-231) into groups of 32 gate rows
- * followed by the matching 32 up rows, so that one output tile holds both
+ * stacked, src/archs/qwen35_text.rs:205-231) into groups of 16 gate rows
+ * followed by the matching 16 up rows, so that one output tile holds both
  * halves.  Load-time only (counterpart of the weight cast in
  * linear_no_bias_dtype, src/archs/modernbert.rs:1043).  `packed` must not
- * alias `w`.  N = 2I. */
+ * alias `w`.  N = 2I, I a multiple of 16. */
 SYS1HIP_API int sys1hip_pack_gated_weight(void* ctx, const uint16_t* w, uint16_t* packed,
                               int64_t N, int64_t K);
 

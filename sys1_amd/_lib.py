@@ -18,7 +18,7 @@ EPI_GEGLU = 2
 EPI_SWIGLU = 4
 EPI_RESIDUAL = 8
 EPI_GELU = 16
-GATE_GROUP = 32
+GATE_GROUP = 16
 
 OK = 0
 EINVAL = -22

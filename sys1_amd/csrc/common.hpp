@@ -60,6 +60,18 @@ __device__ __forceinline__ float epi_apply(float acc, float bias, float resid) {
   return v;
 }
 
+// The register-side part of the non-gated epilogues (everything before the
+// residual add): projection -> bf16, + bias -> bf16, gelu -> bf16.  The
+// residual add then runs on the bf16 value: bf16(v + r).
+template <int EPI>
+__device__ __forceinline__ float epi_pre(float acc, float bias) {
+  float v = round_bf16(acc);
+  if constexpr (EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual)
+    v = round_bf16(v + bias);
+  if constexpr (EPI == kEpiBiasGelu) v = round_bf16(gelu_erf(v));
+  return v;
+}
+
 // One output element of the gated epilogues: gate and up accumulators of the
 // same output column.  GeGLU follows src/kernels/modernbert.cu:9-14 (the
 // activated gate is rounded to the storage type before the multiply);
@@ -94,6 +106,7 @@ struct GemmArgs {
   __bf16* y;            // [M, Nout] ld ldy
   float* ws;            // split-K partials (skinny kernel only)
   unsigned* counters;   // split-K tile arrival counters (skinny kernel only)
+  const void* zeros;    // >= 16 zero bytes: source of K-tail chunks
   int64_t ldx, ldw, ldr, ldy;
   int M, N, K, Nout;
   int splits;           // split-K factor (skinny kernel only)
@@ -140,6 +153,30 @@ __device__ __forceinline__ void load4(const __bf16* p, float v[4], int valid) {
     v[3] = to_f32(i[3]);
   } else {
     for (int j = 0; j < 4; ++j) v[j] = j < valid ? to_f32(p[j]) : 0.0f;
+  }
+}
+
+__device__ __forceinline__ bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+}
+
+// 8 consecutive bf16 of one row: one 16-byte access when all 8 are in range
+// and the address is 16-byte aligned, else element by element.
+__device__ __forceinline__ void store8(__bf16* p, bf16x8 v, int valid) {
+  if (valid >= 8 && aligned16(p)) {
+    *reinterpret_cast<bf16x8*>(p) = v;
+  } else {
+    for (int j = 0; j < valid && j < 8; ++j) p[j] = v[j];
+  }
+}
+
+__device__ __forceinline__ void load8(const __bf16* p, float v[8], int valid) {
+  if (valid >= 8 && aligned16(p)) {
+    const bf16x8 i = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = to_f32(i[j]);
+  } else {
+    for (int j = 0; j < 8; ++j) v[j] = j < valid ? to_f32(p[j]) : 0.0f;
   }
 }
 

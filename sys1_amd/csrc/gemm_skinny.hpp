@@ -2,9 +2,9 @@
 // where the kernel is bound by HBM reads of w[N,K] rather than by MFMA.
 //
 // Work split: a workgroup (4 waves) owns 128 weight rows and one of `splits`
-// contiguous K ranges.  Each wave owns two 16-row fragments of those rows
-// (rows r and r+32 of a 64-row group, so that the gate and up halves of a
-// packed gated weight meet in one lane) and streams them straight from HBM
+// contiguous K ranges.  Each wave owns 32 of those rows as two 16-row
+// fragments (for a packed gated weight: the 16 gate rows and the matching 16
+// up rows, which so meet in one lane) and streams them straight from HBM
 // into registers in the v_mfma_f32_16x16x32_bf16 operand layout: the weight
 // is read once and never staged.  The activations x[0:M, k-slab] are shared
 // by the 4 waves through an LDS double buffer.
@@ -58,12 +58,12 @@ __global__ __launch_bounds__(kSkinnyThreads) void gemm_skinny_kernel(GemmArgs a)
   const int wave = tid >> 6;
   const int l16 = lane & 15;
   const int lk = lane >> 4;  // k-group of 8 within a 32-wide MFMA step
-  // Wave rows: fragment f covers rows n0 + 64*(wave/2) + 16*(wave%2) + 32*f + [0,16).
-  const int rbase = n0 + 64 * (wave >> 1) + 16 * (wave & 1);
+  // Wave rows: fragment f covers rows n0 + 32*wave + 16*f + [0,16).
+  const int rbase = n0 + 32 * wave;
   const __bf16* wrow[2];
 #pragma unroll
   for (int f = 0; f < 2; ++f) {
-    const int row = min(rbase + 32 * f + l16, a.N - 1);
+    const int row = min(rbase + 16 * f + l16, a.N - 1);
     wrow[f] = a.w + (int64_t)row * a.ldw + lk * 8;
   }
 
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void gemm_skinny_kernel(GemmArgs a)
   }
 
   // Epilogue.  Lane holds, per fragment f and token block j: token
-  // m = 16j + lane%16, features rbase + 32f + 4*(lane/16) + [0..3].
+  // m = 16j + lane%16, features rbase + 16f + 4*(lane/16) + [0..3].
   const int nq = 4 * lk;
 #pragma unroll
   for (int j = 0; j < MB16; ++j) {
@@ -184,7 +184,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void gemm_skinny_kernel(GemmArgs a)
     __bf16* yrow = a.y + (int64_t)m * a.ldy;
     if constexpr (epi_gated(EPI)) {
       // Fragment 0 holds gate rows, fragment 1 the matching up rows.
-      const int n = (rbase - 16 * (wave & 1)) / 2 + 16 * (wave & 1) + nq;
+      const int n = rbase / 2 + nq;
       float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = epi_gate<EPI>(acc[0][j][e], acc[1][j][e]);
@@ -193,7 +193,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void gemm_skinny_kernel(GemmArgs a)
       const __bf16* rrow = epi_has_resid<EPI>() ? a.resid + (int64_t)m * a.ldr : nullptr;
 #pragma unroll
       for (int f = 0; f < 2; ++f) {
-        const int n = rbase + 32 * f + nq;
+        const int n = rbase + 16 * f + nq;
         if (n >= a.Nout) continue;
         const int valid = a.Nout - n;
         float b[4] = {0, 0, 0, 0}, r[4] = {0, 0, 0, 0}, v[4];

@@ -21,6 +21,7 @@ namespace {
 constexpr int kVersion = 100;                        // 0.1.0
 constexpr size_t kWorkspaceBytes = 64ull << 20;      // split-K partials
 constexpr int kCounterSlots = 1 << 16;               // split-K arrival counters
+constexpr size_t kZeroBytes = 256;                    // zero page after the counters
 
 thread_local std::string g_last_error;
 
@@ -66,13 +67,16 @@ struct KernelEntry {
   KernelFn fn[kEpiCount];
 };
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, int BK, int ST>
 constexpr KernelEntry tile_entry(const char* name, int occ, float eff) {
   return KernelEntry{name, kTile, BM, BN, WM * WN * 64, 0, occ, eff,
-                     {gemm_tile_kernel<BM, BN, WM, WN, 0>, gemm_tile_kernel<BM, BN, WM, WN, 1>,
-                      gemm_tile_kernel<BM, BN, WM, WN, 2>, gemm_tile_kernel<BM, BN, WM, WN, 3>,
-                      gemm_tile_kernel<BM, BN, WM, WN, 4>, gemm_tile_kernel<BM, BN, WM, WN, 5>,
-                      gemm_tile_kernel<BM, BN, WM, WN, 6>}};
+                     {gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 0>,
+                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 1>,
+                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 2>,
+                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 3>,
+                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 4>,
+                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 5>,
+                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 6>}};
 }
 
 template <int MB16>
@@ -85,11 +89,14 @@ constexpr KernelEntry skinny_entry(const char* name) {
 }
 
 const KernelEntry kKernels[] = {
-    tile_entry<256, 256, 2, 2>("tile_256x256_w2x2", 1, 1.00f),
-    tile_entry<256, 128, 2, 2>("tile_256x128_w2x2", 1, 0.90f),
-    tile_entry<128, 128, 2, 2>("tile_128x128_w2x2", 2, 0.80f),
-    tile_entry<128, 64, 4, 1>("tile_128x64_w4x1", 3, 0.60f),
-    tile_entry<256, 256, 2, 4>("tile_256x256_w2x4", 1, 1.00f),
+    tile_entry<256, 256, 2, 4, 64, 2>("tile_256x256_k64s2_w2x4", 1, 0.80f),
+    tile_entry<256, 160, 4, 1, 64, 2>("tile_256x160_k64s2_w4x1", 1, 0.65f),
+    tile_entry<256, 128, 4, 2, 64, 2>("tile_256x128_k64s2_w4x2", 1, 0.80f),
+    tile_entry<128, 256, 2, 4, 64, 2>("tile_128x256_k64s2_w2x4", 1, 0.80f),
+    tile_entry<128, 192, 4, 2, 64, 2>("tile_128x192_k64s2_w4x2", 1, 0.80f),
+    tile_entry<256, 96, 4, 1, 64, 2>("tile_256x96_k64s2_w4x1", 1, 0.65f),
+    tile_entry<128, 128, 2, 2, 64, 2>("tile_128x128_k64s2_w2x2", 2, 0.80f),
+    tile_entry<128, 64, 2, 1, 64, 2>("tile_128x64_k64s2_w2x1", 2, 0.60f),
     skinny_entry<1>("skinny_m16"),
     skinny_entry<2>("skinny_m32"),
     skinny_entry<4>("skinny_m64"),
@@ -97,8 +104,7 @@ const KernelEntry kKernels[] = {
     skinny_entry<16>("skinny_m256"),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
-constexpr int kFirstSkinny = 5;
-constexpr int kAutoTileCandidates = 4;  // ids 0..3 take part in the automatic choice
+constexpr int kFirstSkinny = 8;
 
 int epi_id_from_flags(int32_t f) {
   switch (f) {
@@ -116,10 +122,11 @@ int epi_id_from_flags(int32_t f) {
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Automatic kernel choice.  M <= 256: the weight-streaming kernel sized to
-// the padded token count.  Otherwise the tile shape that minimises
-// (tile rounds over the CUs) x (tile work) / (relative efficiency).
+// the padded token count.  Otherwise the tile shape with the lowest modelled
+// time: (tiles per CU) x (per-tile cycles), a tile costing the larger of its
+// MFMA cycles (derated by the shape's efficiency) and its operand-load
+// cycles at about 48 B/clk per CU from L2, plus its output write.
 int choose_kernel(const Context* c, int64_t M, int64_t N, int64_t K) {
-  (void)K;
   if (M <= 256) {
     const int64_t blocks = cdiv(M, 16);
     int mb = 1;
@@ -128,13 +135,19 @@ int choose_kernel(const Context* c, int64_t M, int64_t N, int64_t K) {
     for (int b = 1; b < mb; b *= 2) ++id;
     return id;
   }
+  constexpr double kFlopPerClk = 4096.0;  // bf16 MFMA per CU per clock
+  constexpr double kLoadBytesPerClk = 48.0;
+  constexpr double kStoreBytesPerClk = 64.0;
   int best = 0;
   double best_cost = 1e300;
-  for (int id = 0; id < kAutoTileCandidates; ++id) {
+  for (int id = 0; id < kFirstSkinny; ++id) {
     const KernelEntry& e = kKernels[id];
     const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
     const int64_t rounds = cdiv(tiles, (int64_t)c->cus);
-    const double cost = (double)rounds * e.bm * e.bn / e.efficiency;
+    const double mfma = 2.0 * e.bm * e.bn * (double)K / kFlopPerClk / e.efficiency;
+    const double load = (double)(e.bm + e.bn) * K * 2.0 / kLoadBytesPerClk;
+    const double store = 2.0 * e.bm * e.bn / kStoreBytesPerClk;
+    const double cost = (double)rounds * (std::max(mfma, load) + store);
     if (cost < best_cost) best_cost = cost, best = id;
   }
   return best;
@@ -216,8 +229,8 @@ int sys1hip_init(int device, void** out) {
     c->cus = prop.multiProcessorCount;
   if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess ||
       hipMalloc(&c->ws, kWorkspaceBytes) != hipSuccess ||
-      hipMalloc(&c->counters, kCounterSlots * sizeof(unsigned)) != hipSuccess ||
-      hipMemsetAsync(c->counters, 0, kCounterSlots * sizeof(unsigned), c->own) != hipSuccess ||
+      hipMalloc(&c->counters, kCounterSlots * sizeof(unsigned) + kZeroBytes) != hipSuccess ||
+      hipMemsetAsync(c->counters, 0, kCounterSlots * sizeof(unsigned) + kZeroBytes, c->own) != hipSuccess ||
       hipStreamSynchronize(c->own) != hipSuccess) {
     const char* msg = hipGetErrorString(hipGetLastError());
     if (c->counters) (void)hipFree(c->counters);
@@ -297,7 +310,7 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
                 (long long)N, (long long)K);
   const bool gated = epi_gated(epi);
   if (gated && (N % (2 * SYS1HIP_GATE_GROUP)) != 0)
-    return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: gated epilogue needs N %% 64 == 0 (N=%lld)",
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: gated epilogue needs N %% 32 == 0 (N=%lld)",
                 (long long)N);
   const int64_t nout = gated ? N / 2 : N;
   if (M == 0) return SYS1HIP_OK;
@@ -334,6 +347,7 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
   a.y = reinterpret_cast<__bf16*>(y);
   a.ws = c->ws;
   a.counters = c->counters;
+  a.zeros = c->counters + kCounterSlots;
   a.ldx = ldx, a.ldw = ldw, a.ldr = ldr, a.ldy = ldy;
   a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)nout;
   a.splits = 1;
@@ -346,7 +360,9 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
     a.splits = skinny_splits(c, e.mb16, N, K);
     grid = cdiv(N, kSkinnyRows) * a.splits;
   } else {
-    grid = cdiv(M, e.bm) * cdiv(N, e.bn);
+    // Persistent: at most one workgroup per resident slot; each walks its
+    // share of the tiles.
+    grid = std::min<int64_t>(cdiv(M, e.bm) * cdiv(N, e.bn), (int64_t)c->cus * e.occupancy);
   }
   if (grid <= 0 || grid > 0x7fffffff)
     return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: grid of %lld workgroups", (long long)grid);
@@ -360,7 +376,7 @@ int sys1hip_pack_gated_weight(void* ctx, const uint16_t* w, uint16_t* packed, in
   if (!w || !packed) return fail(SYS1HIP_EINVAL, "sys1hip_pack_gated_weight: null pointer");
   if (w == packed) return fail(SYS1HIP_EINVAL, "sys1hip_pack_gated_weight: packed aliases w");
   if (N <= 0 || K <= 0 || N % (2 * SYS1HIP_GATE_GROUP))
-    return fail(SYS1HIP_EINVAL, "sys1hip_pack_gated_weight: need N %% 64 == 0 and K > 0 (N=%lld K=%lld)",
+    return fail(SYS1HIP_EINVAL, "sys1hip_pack_gated_weight: need N %% 32 == 0 and K > 0 (N=%lld K=%lld)",
                 (long long)N, (long long)K);
   if (K % 8) return fail(SYS1HIP_EALIGN, "sys1hip_pack_gated_weight: K must be a multiple of 8");
   if (!aligned16(w) || !aligned16(packed))

@@ -95,7 +95,7 @@ def _call(x=_P, ldx=64, w=_P, ldw=64, bias=None, res=None, ldr=0, y=_P, ldy=64, 
     (dict(epi=_lib.EPI_BIAS), _lib.EINVAL),           # bias flag, no pointer
     (dict(bias=_P), _lib.EINVAL),                     # pointer, no flag
     (dict(epi=_lib.EPI_RESIDUAL), _lib.EINVAL),       # residual flag, no pointer
-    (dict(epi=_lib.EPI_GEGLU, N=96), _lib.EINVAL),    # gated needs N % 64 == 0
+    (dict(epi=_lib.EPI_GEGLU, N=80), _lib.EINVAL),    # gated needs N % 32 == 0
     (dict(ldx=32), _lib.EINVAL),                      # ldx < K
     (dict(ldy=32), _lib.EINVAL),                      # ldy < N
     (dict(K=60, ldx=64, ldw=64), _lib.EALIGN),        # K % 8
@@ -124,7 +124,7 @@ def test_pack_rejects_bad_arguments():
     f = L.sys1hip_pack_gated_weight
     assert f(None, _P, _P + 4096, 64, 64) == _lib.EINVAL
     assert f(_ctx, _P, _P, 64, 64) == _lib.EINVAL          # aliasing
-    assert f(_ctx, _P, _P + 4096, 96, 64) == _lib.EINVAL    # N % 64
+    assert f(_ctx, _P, _P + 4096, 80, 64) == _lib.EINVAL    # N % 32
     assert f(_ctx, _P, _P + 4096, 64, 12) == _lib.EALIGN    # K % 8
     assert f(_ctx, _P + 2, _P + 4096, 64, 64) == _lib.EALIGN
 

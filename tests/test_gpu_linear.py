@@ -198,4 +198,4 @@ def test_python_errors(dev, orc):
         lin(big[:, 1:65])  # 2-byte offset: misaligned rows
     assert e.value.code == -14
     with pytest.raises(ValueError):
-        GatedLinear(torch.zeros(96, 64, dtype=torch.bfloat16, device="cuda:0"), device=dev)
+        GatedLinear(torch.zeros(80, 64, dtype=torch.bfloat16, device="cuda:0"), device=dev)
