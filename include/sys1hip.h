@@ -23,7 +23,8 @@
  *     the context's stream (default: the context's own stream, or the one set
  *     by sys1hip_set_stream).
  *   - One context per stream.  Calls on one context must not overlap: the
- *     split-K workspace held by the context is shared by its calls.
+ *     stream-K workspace and tile counters held by the context are shared
+ *     by its calls.
  *   - Return value 0 on success, a negative SYS1HIP_E* code otherwise; the
  *     message is available from sys1hip_last_error (per calling thread).
  *     This mirrors the reference's native-op error path, which bails with a
@@ -65,7 +66,7 @@ extern "C" {
 SYS1HIP_API int sys1hip_version(void);
 
 /* Create a context on HIP device `device`: selects the device, creates a
- * stream and the split-K workspace.  Counterpart of src/device.rs:43-65
+ * stream and the stream-K workspace.  Counterpart of src/device.rs:43-65
  * (`device::load()` -> Device::new_cuda(0)). */
 SYS1HIP_API int sys1hip_init(int device, void** ctx);
 
@@ -118,6 +119,12 @@ SYS1HIP_API int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K,
 /* Force a kernel id for subsequent calls on this context (-1 = automatic
  * choice).  Used by the tile sweep and by tests that cover every kernel. */
 SYS1HIP_API int sys1hip_set_kernel(void* ctx, int32_t kernel_id);
+
+/* Force the persistent grid size (workgroups) for subsequent calls on this
+ * context (0 = automatic).  Tile shapes launch min(tiles, this); stream-K
+ * shapes divide their (tile, k-tile) iteration space into this many equal
+ * ranges, clamped to the iteration count and to what the workspace holds. */
+SYS1HIP_API int sys1hip_set_grid(void* ctx, int32_t workgroups);
 
 /* Number of kernel ids and the name of one id (for sweeps). */
 SYS1HIP_API int sys1hip_kernel_count(void);

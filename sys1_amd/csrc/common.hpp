@@ -104,12 +104,10 @@ struct GemmArgs {
   const __bf16* bias;   // [Nout] or null
   const __bf16* resid;  // [M, Nout] ld ldr or null
   __bf16* y;            // [M, Nout] ld ldy
-  float* ws;            // split-K partials (skinny kernel only)
-  unsigned* counters;   // split-K tile arrival counters (skinny kernel only)
-  const void* zeros;    // >= 16 zero bytes: source of K-tail chunks
+  float* ws;            // stream-K partials (head/tail slot per workgroup)
+  unsigned* counters;   // stream-K arrival counter per tile (zero between calls)
   int64_t ldx, ldw, ldr, ldy;
   int M, N, K, Nout;
-  int splits;           // split-K factor (skinny kernel only)
 };
 
 // Map the hardware workgroup id to a logical tile id so that each XCD gets a

@@ -11,7 +11,6 @@
 #include <string>
 
 #include "common.hpp"
-#include "gemm_skinny.hpp"
 #include "gemm_tile.hpp"
 
 using namespace sys1;
@@ -19,9 +18,8 @@ using namespace sys1;
 namespace {
 
 constexpr int kVersion = 100;                        // 0.1.0
-constexpr size_t kWorkspaceBytes = 64ull << 20;      // split-K partials
-constexpr int kCounterSlots = 1 << 16;               // split-K arrival counters
-constexpr size_t kZeroBytes = 256;                    // zero page after the counters
+constexpr size_t kWorkspaceBytes = 64ull << 20;      // stream-K partials
+constexpr int kCounterSlots = 1 << 16;               // stream-K arrival counters (tiles)
 
 thread_local std::string g_last_error;
 
@@ -49,62 +47,51 @@ struct Context {
   float* ws = nullptr;
   unsigned* counters = nullptr;
   int forced_kernel = -1;
-  int forced_splits = 0;
+  int forced_grid = 0;
   int cus = 256;
 };
 
 using KernelFn = void (*)(GemmArgs);
 
-enum Kind { kTile = 0, kSkinny = 1 };
-
 struct KernelEntry {
   const char* name;
-  int kind;
-  int bm, bn, threads;  // tile kernels
-  int mb16;             // skinny kernels: padded token blocks of 16
+  int bm, bn, threads;
   int occupancy;        // resident workgroups per CU (LDS/register bound)
-  float efficiency;     // relative per-CU MFMA efficiency, for the heuristic
+  bool streamk;         // stream-K schedule (weight-streaming shapes)
+  float efficiency;     // measured MFMA efficiency of the shape, fitted to a sweep of the
+                        // projection shapes (ModernBERT base/large, Qwen, square)
   KernelFn fn[kEpiCount];
 };
 
-template <int BM, int BN, int WM, int WN, int BK, int ST>
+template <int BM, int BN, int WM, int WN, int ST, bool SK>
 constexpr KernelEntry tile_entry(const char* name, int occ, float eff) {
-  return KernelEntry{name, kTile, BM, BN, WM * WN * 64, 0, occ, eff,
-                     {gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 0>,
-                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 1>,
-                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 2>,
-                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 3>,
-                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 4>,
-                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 5>,
-                      gemm_tile_kernel<BM, BN, WM, WN, BK, ST, 6>}};
+  return KernelEntry{name, BM, BN, WM * WN * 64, occ, SK, eff,
+                     {gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 0>, gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 1>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 2>, gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 3>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 4>, gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 5>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 6>}};
 }
 
-template <int MB16>
-constexpr KernelEntry skinny_entry(const char* name) {
-  return KernelEntry{name, kSkinny, 0, kSkinnyRows, kSkinnyThreads, MB16, 1, 1.0f,
-                     {gemm_skinny_kernel<MB16, 0>, gemm_skinny_kernel<MB16, 1>,
-                      gemm_skinny_kernel<MB16, 2>, gemm_skinny_kernel<MB16, 3>,
-                      gemm_skinny_kernel<MB16, 4>, gemm_skinny_kernel<MB16, 5>,
-                      gemm_skinny_kernel<MB16, 6>}};
-}
-
+// Output-tile shapes.  The first group serves large M (MFMA-bound); the
+// "stream" group serves small M (weight-streaming: BM = padded token count,
+// BN = 256, deep stages, K split over workgroups).
 const KernelEntry kKernels[] = {
-    tile_entry<256, 256, 2, 4, 64, 2>("tile_256x256_k64s2_w2x4", 1, 0.80f),
-    tile_entry<256, 160, 4, 1, 64, 2>("tile_256x160_k64s2_w4x1", 1, 0.65f),
-    tile_entry<256, 128, 4, 2, 64, 2>("tile_256x128_k64s2_w4x2", 1, 0.80f),
-    tile_entry<128, 256, 2, 4, 64, 2>("tile_128x256_k64s2_w2x4", 1, 0.80f),
-    tile_entry<128, 192, 4, 2, 64, 2>("tile_128x192_k64s2_w4x2", 1, 0.80f),
-    tile_entry<256, 96, 4, 1, 64, 2>("tile_256x96_k64s2_w4x1", 1, 0.65f),
-    tile_entry<128, 128, 2, 2, 64, 2>("tile_128x128_k64s2_w2x2", 2, 0.80f),
-    tile_entry<128, 64, 2, 1, 64, 2>("tile_128x64_k64s2_w2x1", 2, 0.60f),
-    skinny_entry<1>("skinny_m16"),
-    skinny_entry<2>("skinny_m32"),
-    skinny_entry<4>("skinny_m64"),
-    skinny_entry<8>("skinny_m128"),
-    skinny_entry<16>("skinny_m256"),
+    tile_entry<256, 256, 2, 4, 2, false>("tile_256x256_s2_w2x4", 1, 1.00f),
+    tile_entry<256, 160, 4, 1, 2, false>("tile_256x160_s2_w4x1", 1, 0.37f),
+    tile_entry<256, 128, 4, 2, 2, false>("tile_256x128_s2_w4x2", 1, 0.77f),
+    tile_entry<128, 256, 2, 4, 2, false>("tile_128x256_s2_w2x4", 1, 0.44f),
+    tile_entry<128, 192, 4, 2, 2, false>("tile_128x192_s2_w4x2", 1, 0.66f),
+    tile_entry<256, 96, 4, 1, 2, false>("tile_256x96_s2_w4x1", 1, 0.41f),
+    tile_entry<128, 128, 2, 2, 2, false>("tile_128x128_s2_w2x2", 2, 0.93f),
+    tile_entry<128, 64, 2, 1, 2, false>("tile_128x64_s2_w2x1", 2, 0.38f),
+    tile_entry<32, 256, 1, 4, 4, true>("stream_32x256_s4_w1x4", 1, 0.50f),
+    tile_entry<64, 256, 2, 4, 3, true>("stream_64x256_s3_w2x4", 1, 0.60f),
+    tile_entry<128, 128, 2, 2, 2, true>("stream_128x128_s2_w2x2", 2, 0.90f),
+    tile_entry<128, 256, 2, 4, 2, true>("stream_128x256_s2_w2x4", 1, 0.80f),
+    tile_entry<256, 128, 4, 2, 2, true>("stream_256x128_s2_w4x2", 1, 0.77f),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
-constexpr int kFirstSkinny = 8;
+constexpr int kFirstStream = 8;
 
 int epi_id_from_flags(int32_t f) {
   switch (f) {
@@ -121,55 +108,84 @@ int epi_id_from_flags(int32_t f) {
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Automatic kernel choice.  M <= 256: the weight-streaming kernel sized to
-// the padded token count.  Otherwise the tile shape with the lowest modelled
-// time: (tiles per CU) x (per-tile cycles), a tile costing the larger of its
-// MFMA cycles (derated by the shape's efficiency) and its operand-load
-// cycles at about 48 B/clk per CU from L2, plus its output write.
-int choose_kernel(const Context* c, int64_t M, int64_t N, int64_t K) {
-  if (M <= 256) {
-    const int64_t blocks = cdiv(M, 16);
-    int mb = 1;
-    while (mb < blocks) mb *= 2;
-    int id = kFirstSkinny;
-    for (int b = 1; b < mb; b *= 2) ++id;
-    return id;
+// Modelled time (in CU clocks) of a projection on kernel `e` launched on
+// `grid` workgroups.  Tile shapes: (tile rounds over the resident slots) x
+// (per-tile cycles).  Stream-K shapes: the iteration space divided evenly
+// over the grid, plus the partial-tile fix-up traffic and latency.  A tile's
+// cycles are the larger of its MFMA cycles (derated by the shape's measured
+// efficiency) and its operand loads at about 48 B/clk per CU from L2, plus
+// its output write; the whole call is bounded below by the chip's HBM time
+// for the weights.
+constexpr double kFlopPerClk = 4096.0;      // bf16 MFMA per CU per clock
+constexpr double kLoadBytesPerClk = 48.0;   // L2 -> CU
+constexpr double kStoreBytesPerClk = 64.0;
+constexpr double kHbmBytesPerClk = 3000.0;  // ~6.6 TB/s sustained at ~2.2 GHz, whole chip
+constexpr double kFixupClk = 6000.0;        // partial write + arrival + reduction latency
+
+double model_cost(const Context* c, const KernelEntry& e, int64_t M, int64_t N, int64_t K,
+                  int64_t grid) {
+  const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
+  const int64_t kts = cdiv(K, 64);
+  const double mfma = 2.0 * e.bm * e.bn * 64.0 / kFlopPerClk / e.efficiency;  // per k-tile
+  const double load = (double)(e.bm + e.bn) * 64.0 * 2.0 / kLoadBytesPerClk;
+  const double per_kt = std::max(mfma, load);
+  const double store = 2.0 * e.bm * e.bn / kStoreBytesPerClk;
+  const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk;
+  double t;
+  if (e.streamk) {
+    const double iters = (double)cdiv(tiles * kts, grid);
+    const double tiles_per_wg = (double)cdiv(tiles, grid) + 1.0;
+    const bool partial = grid > tiles || (tiles * kts) % grid != 0;
+    t = iters * per_kt + tiles_per_wg * store + (partial ? kFixupClk : 0.0);
+    const double fix = partial ? 2.0 * 2.0 * grid * e.bm * e.bn * 4.0 / kHbmBytesPerClk : 0.0;
+    return std::max(t, hbm) + fix;
   }
-  constexpr double kFlopPerClk = 4096.0;  // bf16 MFMA per CU per clock
-  constexpr double kLoadBytesPerClk = 48.0;
-  constexpr double kStoreBytesPerClk = 64.0;
-  int best = 0;
-  double best_cost = 1e300;
-  for (int id = 0; id < kFirstSkinny; ++id) {
-    const KernelEntry& e = kKernels[id];
-    const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
-    const int64_t rounds = cdiv(tiles, (int64_t)c->cus);
-    const double mfma = 2.0 * e.bm * e.bn * (double)K / kFlopPerClk / e.efficiency;
-    const double load = (double)(e.bm + e.bn) * K * 2.0 / kLoadBytesPerClk;
-    const double store = 2.0 * e.bm * e.bn / kStoreBytesPerClk;
-    const double cost = (double)rounds * (std::max(mfma, load) + store);
-    if (cost < best_cost) best_cost = cost, best = id;
-  }
-  return best;
+  const int64_t rounds = cdiv(tiles, (int64_t)c->cus * e.occupancy) * e.occupancy;
+  t = (double)rounds * (kts * per_kt + store);
+  return std::max(t, hbm);
 }
 
-int skinny_splits(const Context* c, int mb16, int64_t N, int64_t K) {
-  const int64_t tiles = cdiv(N, kSkinnyRows);
-  const int ks = mb16 >= 16 ? 64 : 128;
-  const int64_t nslab = cdiv(K, ks);
-  int64_t s;
-  if (c->forced_splits > 0) {
-    s = c->forced_splits;
-  } else {
-    // Aim for about two workgroups per CU; keep at least 2 slabs per split.
-    s = cdiv(2 * (int64_t)c->cus, tiles);
-    s = std::min<int64_t>(s, std::max<int64_t>(1, nslab / 2));
+int64_t max_grid(const Context* c, const KernelEntry& e, int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
+  int64_t g = (int64_t)c->cus * e.occupancy;
+  if (!e.streamk) return std::min(g, tiles);
+  g = std::min(g, tiles * cdiv(K, 64));
+  while (g > 1 && 2 * g * e.bm * e.bn * 4 > (int64_t)kWorkspaceBytes) --g;
+  return g;
+}
+
+// Automatic choice of kernel and grid: the lowest modelled time over the
+// shapes that fit M (stream shapes only for M up to their BM; tile shapes
+// only above 128 tokens).  Stream-K grids from a quarter of the CUs up to all
+// of them are tried.
+void choose(const Context* c, int64_t M, int64_t N, int64_t K, int* kernel, int* grid) {
+  double best = 1e300;
+  *kernel = 0;
+  *grid = 1;
+  for (int id = 0; id < kNumKernels; ++id) {
+    const KernelEntry& e = kKernels[id];
+    if (e.streamk && M > e.bm) continue;
+    if (!e.streamk && M <= 128) continue;
+    const int64_t gmax = max_grid(c, e, M, N, K);
+    const int64_t gmin = e.streamk ? std::max<int64_t>(1, gmax / 4) : gmax;
+    for (int64_t g = gmax; g >= gmin; g -= std::max<int64_t>(1, gmax / 16)) {
+      const double cost = model_cost(c, e, M, N, K, g);
+      if (cost < best * 0.999) best = cost, *kernel = id, *grid = (int)g;
+    }
   }
-  s = std::max<int64_t>(1, std::min<int64_t>(s, nslab));
-  const int64_t tile_bytes = (int64_t)4 * 2 * mb16 * 64 * 16;
-  if (tiles > kCounterSlots) return 1;
-  while (s > 1 && s * tiles * tile_bytes > (int64_t)kWorkspaceBytes) --s;
-  return (int)s;
+}
+
+// Kernel and grid for a call: the automatic choice, or a forced kernel id
+// and/or a forced grid size.
+void resolve(const Context* c, int64_t M, int64_t N, int64_t K, int* kernel, int* grid) {
+  if (c->forced_kernel < 0) {
+    choose(c, M, N, K, kernel, grid);
+  } else {
+    *kernel = c->forced_kernel;
+    *grid = (int)max_grid(c, kKernels[*kernel], M, N, K);
+  }
+  if (c->forced_grid > 0)
+    *grid = (int)std::min<int64_t>(c->forced_grid, max_grid(c, kKernels[*kernel], M, N, K));
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -229,8 +245,8 @@ int sys1hip_init(int device, void** out) {
     c->cus = prop.multiProcessorCount;
   if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess ||
       hipMalloc(&c->ws, kWorkspaceBytes) != hipSuccess ||
-      hipMalloc(&c->counters, kCounterSlots * sizeof(unsigned) + kZeroBytes) != hipSuccess ||
-      hipMemsetAsync(c->counters, 0, kCounterSlots * sizeof(unsigned) + kZeroBytes, c->own) != hipSuccess ||
+      hipMalloc(&c->counters, kCounterSlots * sizeof(unsigned)) != hipSuccess ||
+      hipMemsetAsync(c->counters, 0, kCounterSlots * sizeof(unsigned), c->own) != hipSuccess ||
       hipStreamSynchronize(c->own) != hipSuccess) {
     const char* msg = hipGetErrorString(hipGetLastError());
     if (c->counters) (void)hipFree(c->counters);
@@ -239,7 +255,6 @@ int sys1hip_init(int device, void** out) {
     delete c;
     return fail(SYS1HIP_EDEVICE, "sys1hip_init: device set-up failed (%s)", msg);
   }
-  if (const char* s = getenv("SYS1HIP_SPLITS")) c->forced_splits = atoi(s);
   c->stream = c->own;
   *out = c;
   return SYS1HIP_OK;
@@ -282,17 +297,26 @@ int sys1hip_set_kernel(void* ctx, int32_t id) {
   return SYS1HIP_OK;
 }
 
+int sys1hip_set_grid(void* ctx, int32_t workgroups) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_set_grid: null context");
+  if (workgroups < 0) return fail(SYS1HIP_EINVAL, "sys1hip_set_grid: negative grid %d", workgroups);
+  static_cast<Context*>(ctx)->forced_grid = workgroups;
+  return SYS1HIP_OK;
+}
+
 int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epilogue, char* name,
                          int64_t cap) {
   if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: null context");
   if (epi_id_from_flags(epilogue) < 0)
     return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: unsupported epilogue flags %d", epilogue);
   const Context* c = static_cast<const Context*>(ctx);
-  const int id = c->forced_kernel >= 0 ? c->forced_kernel : choose_kernel(c, M, N, K);
+  if (M <= 0 || N <= 0 || K <= 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: bad shape");
+  int id, grid;
+  resolve(c, M, N, K, &id, &grid);
   if (name && cap > 0) {
     std::string s = kKernels[id].name;
-    if (kKernels[id].kind == kSkinny)
-      s += "_s" + std::to_string(skinny_splits(c, kKernels[id].mb16, N, K));
+    s += "_g" + std::to_string(grid);
     snprintf(name, (size_t)cap, "%s", s.c_str());
   }
   return id;
@@ -336,8 +360,11 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
 
   int rc = use_device(c);
   if (rc) return rc;
-  const int id = c->forced_kernel >= 0 ? c->forced_kernel : choose_kernel(c, M, N, K);
+  int id, grid;
+  resolve(c, M, N, K, &id, &grid);
   const KernelEntry& e = kKernels[id];
+  if (e.streamk && cdiv(M, e.bm) * cdiv(N, e.bn) > kCounterSlots)
+    return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: more tiles than stream-K counters");
 
   GemmArgs a;
   a.x = reinterpret_cast<const __bf16*>(x);
@@ -347,23 +374,9 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
   a.y = reinterpret_cast<__bf16*>(y);
   a.ws = c->ws;
   a.counters = c->counters;
-  a.zeros = c->counters + kCounterSlots;
   a.ldx = ldx, a.ldw = ldw, a.ldr = ldr, a.ldy = ldy;
   a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)nout;
-  a.splits = 1;
 
-  int64_t grid;
-  if (e.kind == kSkinny) {
-    if (M > 16 * e.mb16)
-      return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: kernel %s takes M <= %d, got %lld", e.name,
-                  16 * e.mb16, (long long)M);
-    a.splits = skinny_splits(c, e.mb16, N, K);
-    grid = cdiv(N, kSkinnyRows) * a.splits;
-  } else {
-    // Persistent: at most one workgroup per resident slot; each walks its
-    // share of the tiles.
-    grid = std::min<int64_t>(cdiv(M, e.bm) * cdiv(N, e.bn), (int64_t)c->cus * e.occupancy);
-  }
   if (grid <= 0 || grid > 0x7fffffff)
     return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: grid of %lld workgroups", (long long)grid);
   hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)grid), dim3(e.threads), 0, c->stream, a);

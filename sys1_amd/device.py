@@ -41,6 +41,10 @@ class HipDevice:
         """Force one kernel id (-1: automatic choice)."""
         _lib.check(self._L.sys1hip_set_kernel(self.ctx, int(kernel_id)), self.ctx)
 
+    def set_grid(self, workgroups: int) -> None:
+        """Force the persistent grid size (0: automatic)."""
+        _lib.check(self._L.sys1hip_set_grid(self.ctx, int(workgroups)), self.ctx)
+
     def query_kernel(self, M: int, N: int, K: int, epilogue: int = 0) -> tuple[int, str]:
         buf = ctypes.create_string_buffer(96)
         kid = _lib.check(self._L.sys1hip_query_kernel(self.ctx, M, N, K, epilogue, buf, 96), self.ctx)

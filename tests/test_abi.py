@@ -36,7 +36,7 @@ def test_version_and_kernel_table():
     assert L.sys1hip_version() == 100
     names = _lib.kernel_names()
     assert len(names) == L.sys1hip_kernel_count() >= 6
-    assert any(n.startswith("tile_") for n in names) and any(n.startswith("skinny_") for n in names)
+    assert any(n.startswith("tile_") for n in names) and any(n.startswith("stream_") for n in names)
     assert L.sys1hip_kernel_name(-1) is None and L.sys1hip_kernel_name(len(names)) is None
 
 
@@ -132,4 +132,6 @@ def test_pack_rejects_bad_arguments():
 def test_query_and_set_kernel_validate():
     L = _lib.load()
     assert L.sys1hip_set_kernel(None, 0) == _lib.EINVAL
+    assert L.sys1hip_set_grid(None, 0) == _lib.EINVAL
+    assert L.sys1hip_set_grid(_ctx, -1) == _lib.EINVAL
     assert L.sys1hip_query_kernel(None, 1, 1, 8, 0, None, 0) == _lib.EINVAL

@@ -73,9 +73,9 @@ def test_every_kernel_every_epilogue(dev, orc, kid, name):
     """Force each kernel id and check every epilogue on ragged shapes."""
     from sys1_amd import _lib
     from sys1_amd.linear import GatedLinear, Linear
-    if name.startswith("skinny_"):
-        cap = int(name.split("_m")[1])
-        Ms = sorted({max(1, cap // 2 + 3), cap})
+    if name.startswith("stream_"):
+        cap = int(name.split("_")[1].split("x")[0])
+        Ms = sorted({max(1, cap // 2 + 3), cap, 300})
     else:
         Ms = [300, 513]
     dev.set_kernel(kid)
@@ -166,20 +166,43 @@ def test_tiny_output_width(dev, orc):
     assert_parity(y, orc.linear_f32(x, w, b), "N=1")
 
 
-def test_split_k_is_deterministic_and_rearms(dev, orc):
-    """Split-K partial sums are reduced in split order: repeated calls are
-    bit-identical, and the tile counters re-arm between calls of different
-    shapes."""
+def test_stream_k_is_deterministic_and_rearms(dev, orc):
+    """Stream-K partial tiles are reduced in workgroup order: repeated calls
+    are bit-identical, every forced grid agrees with the oracle, and the
+    tile counters re-arm between calls of different shapes."""
     from sys1_amd.linear import Linear
     outs = []
-    for (M, N, K) in [(64, 1024, 4096), (32, 768, 2048), (64, 1024, 4096), (200, 4096, 2048)]:
+    for (M, N, K) in [(64, 1024, 4096), (32, 768, 2048), (64, 1024, 4096), (200, 4096, 2048),
+                      (128, 520, 1000)]:
         _, name = dev.query_kernel(M, N, K)
-        print(f"[gpu] split-k M={M} N={N} K={K} {name}", flush=True)
+        print(f"[gpu] stream-k M={M} N={N} K={K} {name}", flush=True)
         x, w = _inputs(orc, M, N, K, 50 + M + N)
         y = to_np(Linear(to_gpu_bf16(w, torch), device=dev)(to_gpu_bf16(x, torch)))
-        assert_parity(y, orc.linear_f32(x, w), f"split-k {M}x{N}x{K}")
+        assert_parity(y, orc.linear_f32(x, w), f"stream-k {M}x{N}x{K}")
         outs.append(y)
     np.testing.assert_array_equal(outs[0], outs[2])
+    # forced grid sizes on a stream-K kernel: every head/tail/fix-up pattern
+    from sys1_amd import kernel_names
+    kid = kernel_names().index("stream_64x256_s3_w2x4")
+    M, N, K = 50, 700, 1024
+    x, w = _inputs(orc, M, N, K, 77)
+    ref = orc.linear_f32(x, w)
+    dev.set_kernel(kid)
+    try:
+        prev = None
+        for g in (1, 2, 3, 5, 7, 16, 48, 1000):
+            dev.set_grid(g)
+            print(f"[gpu] forced grid={g} {dev.query_kernel(M, N, K)[1]}", flush=True)
+            y = to_np(Linear(to_gpu_bf16(w, torch), device=dev)(to_gpu_bf16(x, torch)))
+            assert_parity(y, ref, f"grid={g}")
+            if prev is not None:
+                assert np.abs(y - prev).max() <= 2 * np.abs(ref).max() * 2 ** -8
+            prev = y
+            z = to_np(Linear(to_gpu_bf16(w, torch), device=dev)(to_gpu_bf16(x, torch)))
+            np.testing.assert_array_equal(y, z)  # deterministic, counters re-armed
+    finally:
+        dev.set_grid(0)
+        dev.set_kernel(-1)
 
 
 def test_python_errors(dev, orc):

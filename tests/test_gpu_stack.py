@@ -1,0 +1,304 @@
+"""GPU parity of whole projection stacks (the callers of the hot path)
+against the CPU oracle, through the C ABI.
+
+  - every projection of the chain, on the inputs the GPU chain actually fed
+    it, against the oracle's f32 projection (rel. Frobenius <= 1e-2, max-abs
+    <= 2e-2 * max|ref|);
+  - the final hidden state of the bf16 GPU chain against the oracle's f32
+    chain from the same seeded f32 inputs (reported, and bounded);
+  - the decision logits of the Laya scorer (src/models/laya.rs:510-520) at
+    option-marker rows: within 2e-2 of the oracle's, and the argmax
+    (src/models/laya.rs:909-916 tie rule) identical for every request whose
+    f32 decision is not a near-tie inside the bf16 noise band.
+
+Chains apply the reference's pre-block norms (ModernBERT's bias-free
+LayerNorm, Qwen's RMSNorm) as glue on both sides -- without them the
+norm-free chain grows without bound and no precision comparison is
+meaningful.  The attention stand-in (V block of Wqkv feeds Wo; z block feeds
+out_proj; q block feeds o_proj) is the one the stacks use.
+"""
+import numpy as np
+import pytest
+
+from gpu_helpers import assert_parity, parity, to_gpu_bf16, to_np
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from sys1_amd.device import HipDevice
+    return HipDevice(0)
+
+
+def _weights(orc, cfg, seed):
+    return [[orc.fill_normal((p.N, p.K), seed + 1000 * li + pi, 0.02) for pi, p in enumerate(layer)]
+            for li, layer in enumerate(cfg.layers)]
+
+
+def _norm_gpu(h, kind):
+    """Pre-block norm as glue (not a projection): ModernBERT's bias-free
+    LayerNorm (src/archs/modernbert.rs:1005-1034, weight 1) or Qwen's RMSNorm
+    with alpha = 1 + w, w = 0 (src/archs/qwen35_text.rs:178-203), in f32."""
+    hf = h.float()
+    if kind == "ln":
+        out = torch.nn.functional.layer_norm(hf, (hf.shape[-1],), eps=1e-5)
+    else:
+        out = hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    return out.to(torch.bfloat16)
+
+
+def _norm_ref(orc, h, kind):
+    h = np.asarray(h, np.float32)
+    if kind == "ln":
+        return orc.layer_norm(h, np.ones(h.shape[-1], np.float32), None, 1e-5)
+    hd = h.astype(np.float64)
+    return (hd / np.sqrt((hd ** 2).mean(-1, keepdims=True) + 1e-6)).astype(np.float32)
+
+
+def _project_ref(orc, p, src, w, resid):
+    """The oracle's f32 projection of one stack entry (with its epilogue)."""
+    from sys1_amd import _lib
+    proj = orc.linear_f32(src, w)
+    if p.epi == _lib.EPI_GEGLU:
+        return orc.geglu(proj)
+    if p.epi == _lib.EPI_SWIGLU:
+        I = p.N // 2
+        return orc.swiglu(proj[:, :I], proj[:, I:])
+    return proj + resid if p.resid else proj
+
+
+def _chain_per_projection(orc, dev, cfg, x, ws, norm):
+    """Run the stack projection by projection on the GPU (sys1_amd.linear
+    modules) and check each output against the oracle on the same input."""
+    from sys1_amd import _lib
+    from sys1_amd.linear import GatedLinear, Linear
+    M = x.shape[0]
+    h = to_gpu_bf16(x, torch)
+    mix = None
+    worst = 0.0
+    for li, layer in enumerate(cfg.layers):
+        for pi, p in enumerate(layer):
+            w = ws[li][pi]
+            if p.src == "h":
+                src = _norm_gpu(h, norm) if norm else h
+            else:
+                src = mix[:, p.src_off:p.src_off + p.K]
+            wg = to_gpu_bf16(w, torch)
+            if p.epi in (_lib.EPI_GEGLU, _lib.EPI_SWIGLU):
+                out = GatedLinear(wg, "gelu" if p.epi == _lib.EPI_GEGLU else "silu", device=dev)(src)
+            elif p.resid:
+                out = Linear(wg, device=dev)(src, residual=h)
+            else:
+                out = Linear(wg, device=dev)(src)
+            ref = _project_ref(orc, p, to_np(src), w, to_np(h) if p.resid else None)
+            rel, _ = assert_parity(to_np(out), ref, f"layer {li} {p.name} M={M}")
+            worst = max(worst, rel)
+            if p.dst == "h":
+                h = out
+            else:
+                mix = out
+    return h, worst
+
+
+def _oracle_chain(orc, cfg, x, ws, norm):
+    """The same chain in f32 end to end (the reference's f32 CPU path)."""
+    h = x.astype(np.float32)
+    mix = None
+    for li, layer in enumerate(cfg.layers):
+        for pi, p in enumerate(layer):
+            if p.src == "h":
+                src = _norm_ref(orc, h, norm) if norm else h
+            else:
+                src = np.ascontiguousarray(mix[:, p.src_off:p.src_off + p.K])
+            out = _project_ref(orc, p, src, ws[li][pi], h if p.resid else None)
+            if p.dst == "h":
+                h = out
+            else:
+                mix = out
+    return h
+
+
+def _scorer(orc, H, seed):
+    g = orc.fill_normal((H,), seed, 0.1) + 1.0
+    b = orc.fill_normal((H,), seed + 1, 0.1)
+    w_in = orc.fill_normal((H, H), seed + 2, 1.0 / np.sqrt(H))
+    b_in = orc.fill_normal((H,), seed + 3, 0.1)
+    w_out = orc.fill_normal((1, H), seed + 4, 1.0 / np.sqrt(H))
+    b_out = orc.fill_normal((1,), seed + 5, 0.1)
+    return g, b, w_in, b_in, w_out, b_out
+
+
+def _gpu_scorer(dev, hidden_rows_gpu, params):
+    """LN (torch, f32: not a projection) -> Linear+bias+gelu (fused) ->
+    Linear+bias, the last two on the HIP kernels."""
+    from sys1_amd.linear import Linear
+    g, b, w_in, b_in, w_out, b_out = params
+    z = torch.nn.functional.layer_norm(hidden_rows_gpu.float(), (g.size,),
+                                       torch.from_numpy(g).cuda(), torch.from_numpy(b).cuda(), 1e-5)
+    z = z.to(torch.bfloat16)
+    z = Linear(to_gpu_bf16(w_in, torch), to_gpu_bf16(b_in, torch), device=dev)(z, gelu=True)
+    return to_np(Linear(to_gpu_bf16(w_out, torch), to_gpu_bf16(b_out, torch), device=dev)(z))[:, 0]
+
+
+def _markers(lengths, options, seed):
+    """Option-marker rows: `options` distinct positions inside each sequence."""
+    rng = np.random.default_rng(seed)
+    rows, off = [], 0
+    for L in lengths:
+        rows.append(off + np.sort(rng.choice(L, size=min(options, L), replace=False)))
+        off += L
+    return rows
+
+
+def _check_argmax(orc, dev, h_gpu, h_ref, lengths, H, seed):
+    """Scorer at the option markers after the encoder's final norm
+    (src/archs/modernbert.rs:988).  The argmax must match the f32 oracle for
+    every request whose f32 top-2 margin exceeds the bf16 noise band (3x the
+    RMS logit error measured over all options).  Requests inside the band are
+    near-ties that bf16 arithmetic cannot order -- with random weights the
+    gap between two options is sometimes below 1% of the logits' scale --
+    they are counted and reported, and at least 75% of the requests must be
+    decisive so the check cannot pass vacuously."""
+    params = _scorer(orc, H, seed)
+    marks = _markers(lengths, 4, seed)
+    flat = np.concatenate(marks)
+    logits_ref = orc.laya_scorer_f32(_norm_ref(orc, h_ref[flat], "ln"), *params)
+    logits_gpu = _gpu_scorer(dev, _norm_gpu(h_gpu[torch.from_numpy(flat).cuda()], "ln"), params)
+    rel = parity(logits_gpu, logits_ref)[0]
+    assert rel <= 2e-2, f"logit rel err {rel:.3e}"
+    band = 3.0 * float(np.sqrt(np.mean((logits_gpu - logits_ref) ** 2)))
+    off = agree = decisive = decisive_agree = 0
+    for r in marks:
+        lr = logits_ref[off:off + len(r)]
+        lg = logits_gpu[off:off + len(r)]
+        off += len(r)
+        s = np.sort(lr)
+        margin = float(s[-1] - s[-2]) if len(s) > 1 else np.inf
+        same = orc.argmax(lr) == orc.argmax(lg)
+        agree += same
+        if margin > band:
+            decisive += 1
+            decisive_agree += same
+    print(f"[gpu] argmax agreement {agree}/{len(marks)} overall, {decisive_agree}/{decisive} on "
+          f"requests with f32 margin > {band:.2e} (3x RMS logit error); logit rel err {rel:.3e}",
+          flush=True)
+    assert decisive_agree == decisive
+    assert decisive >= 0.75 * len(marks)
+
+
+# The bf16 chain vs the f32 chain over 22 normed layers: about 1.3e-2 from
+# bf16 rounding alone (emulating the bf16 chain with the oracle gives the same).
+CHAIN_TOL = 3e-2
+
+
+def test_modernbert_base_cfg1_chain(dev, orc):
+    """BASELINE config 1 shapes: 22 layers, hidden 768, M = 8 x 128 = 1024."""
+    from sys1_amd.stacks import CONFIGS
+    cfg = CONFIGS["modernbert-base"]()
+    lengths = [128] * 8
+    M = sum(lengths)
+    print(f"[gpu] modernbert-base chain M={M}", flush=True)
+    x = orc.fill_normal((M, 768), 7)
+    ws = _weights(orc, cfg, 100)
+    h_gpu, worst = _chain_per_projection(orc, dev, cfg, x, ws, "ln")
+    h_ref = _oracle_chain(orc, cfg, x, ws, "ln")
+    rel, mx = parity(to_np(h_gpu), h_ref)
+    print(f"[gpu] cfg1 final hidden vs f32 chain: rel_fro={rel:.3e} max={mx:.3e}; "
+          f"worst per-projection rel_fro={worst:.3e}", flush=True)
+    assert rel < CHAIN_TOL
+    _check_argmax(orc, dev, h_gpu, h_ref, lengths, 768, 11)
+
+
+def test_modernbert_base_ragged_chain(dev, orc):
+    """lengths U[16,512] packed to an 8192-token budget."""
+    from sys1_amd.batching import draw_lengths
+    from sys1_amd.stacks import CONFIGS
+    cfg = CONFIGS["modernbert-base"]()
+    lengths = draw_lengths(3, 16, 512, 8192)
+    M = int(lengths.sum())
+    print(f"[gpu] modernbert-base ragged chain M={M} ({len(lengths)} sequences)", flush=True)
+    x = orc.fill_normal((M, 768), 9)
+    ws = _weights(orc, cfg, 300)
+    h_gpu, worst = _chain_per_projection(orc, dev, cfg, x, ws, "ln")
+    h_ref = _oracle_chain(orc, cfg, x, ws, "ln")
+    rel, mx = parity(to_np(h_gpu), h_ref)
+    print(f"[gpu] cfg2 final hidden vs f32 chain: rel_fro={rel:.3e} max={mx:.3e}; "
+          f"worst per-projection rel_fro={worst:.3e}", flush=True)
+    assert rel < CHAIN_TOL
+    _check_argmax(orc, dev, h_gpu, h_ref, lengths, 768, 13)
+
+
+def test_projection_stack_matches_module_chain(dev, orc):
+    """The fused ProjectionStack (the bench's path: one C call per
+    projection, in-place residual, V-slice stand-in) equals the
+    module-by-module chain bit for bit on a ragged 8192-budget batch."""
+    from sys1_amd.batching import draw_lengths
+    from sys1_amd.linear import GatedLinear, Linear
+    from sys1_amd.stacks import CONFIGS, ProjectionStack, modernbert
+    cfg = modernbert(768, 1152, 3, "modernbert-base-3")
+    M = int(draw_lengths(5, 16, 512, 8192).sum())
+    x = to_gpu_bf16(orc.fill_normal((M, 768), 3), torch)
+    ws = [[(torch.randn(p.N, p.K, device="cuda") * 0.02).to(torch.bfloat16) for p in layer]
+          for layer in cfg.layers]
+    stack = ProjectionStack(cfg, dev, M, weights=ws)
+    out = stack.forward(x, M).clone()
+    h = x
+    for (wqkv, wo, wi, wo2) in ws:
+        qkv = Linear(wqkv, device=dev)(h)
+        h = Linear(wo, device=dev)(qkv[:, 1536:], residual=h)
+        g = GatedLinear(wi, "gelu", device=dev)(h)
+        h = Linear(wo2, device=dev)(g, residual=h)
+    assert torch.equal(out, h)
+
+
+@pytest.mark.parametrize("M", [64, 1024])
+def test_modernbert_large_chain(dev, orc, M):
+    """BASELINE config 3 shapes (hidden 1024, GeGLU 2x2624), first 4 layers,
+    skinny (M=64) and tiled (M=1024) regimes."""
+    from sys1_amd.stacks import modernbert
+    cfg = modernbert(1024, 2624, 4, "modernbert-large-4")
+    print(f"[gpu] modernbert-large 4 layers M={M}", flush=True)
+    x = orc.fill_normal((M, 1024), 21)
+    ws = _weights(orc, cfg, 500)
+    h_gpu, worst = _chain_per_projection(orc, dev, cfg, x, ws, "ln")
+    rel, _ = parity(to_np(h_gpu), _oracle_chain(orc, cfg, x, ws, "ln"))
+    print(f"[gpu] large M={M}: final rel_fro={rel:.3e}, worst per-projection {worst:.3e}", flush=True)
+    assert rel < CHAIN_TOL
+
+
+@pytest.mark.parametrize("name,M", [("qwen35-small", 256), ("qwen35-small", 1000),
+                                    ("qwen35-27b", 128)])
+def test_qwen_layers(dev, orc, name, M):
+    """One DeltaNet layer and one gated-attention layer of the Qwen3.5-style
+    configs (4 and 5), at their real projection shapes, per projection."""
+    from sys1_amd.stacks import CONFIGS, StackConfig
+    full = CONFIGS[name]()
+    cfg = StackConfig(name, full.hidden, [full.layers[0], full.layers[3]])
+    print(f"[gpu] {name} DeltaNet + attention layer M={M}", flush=True)
+    x = orc.fill_normal((M, full.hidden), 31)
+    ws = _weights(orc, cfg, 700)
+    h_gpu, worst = _chain_per_projection(orc, dev, cfg, x, ws, "rms")
+    rel, _ = parity(to_np(h_gpu), _oracle_chain(orc, cfg, x, ws, "rms"))
+    print(f"[gpu] {name} M={M}: final rel_fro={rel:.3e}, worst per-projection rel_fro={worst:.3e}",
+          flush=True)
+    assert rel < CHAIN_TOL
+
+
+def test_row_permutation_is_exact(dev, orc):
+    """Row independence: permuting the packed tokens permutes the outputs
+    bit for bit (same kernel, same split), which is what makes packing the
+    reference's padded rectangle exact."""
+    from sys1_amd.linear import GatedLinear, Linear
+    for (M, N, K) in [(8000, 2304, 768), (200, 3072, 1024)]:
+        x = torch.randn(M, K, device="cuda").to(torch.bfloat16)
+        w = (torch.randn(N, K, device="cuda") * 0.02).to(torch.bfloat16)
+        perm = torch.randperm(M, device="cuda")
+        lin = Linear(w, device=dev)
+        assert torch.equal(lin(x)[perm], lin(x[perm]))
+        g = GatedLinear(w, "gelu", device=dev)
+        assert torch.equal(g(x)[perm], g(x[perm]))
