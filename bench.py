@@ -53,7 +53,46 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
+                    help="after the run, 8 bf16 negations of MIB MiB (read MIB, write MIB): the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
+                    help="reduce rocprofv3 counter_collection.csv files to per-kernel averages "
+                         "per dispatch and exit (no GPU use)")
     return ap.parse_args()
+
+
+def pmc_summary(paths: list[str]) -> None:
+    """Average counter value per dispatch, per kernel name, over the given
+    rocprofv3 --pmc CSV files (rows are one counter of one dispatch; a
+    counter collected per XCD/SE instance is summed within the dispatch)."""
+    import csv
+    import collections
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            per[(r["Kernel_Name"], r["Dispatch_Id"])][r["Counter_Name"]] += float(r["Counter_Value"])
+    by_kernel = collections.defaultdict(lambda: collections.defaultdict(list))
+    for (name, _), counters in per.items():
+        for c, v in counters.items():
+            by_kernel[name][c].append(v)
+    for name in sorted(by_kernel):
+        cs = by_kernel[name]
+        n = max(len(v) for v in cs.values())
+        vals = ", ".join(f"{c}={sum(v) / len(v):.6g}" for c, v in sorted(cs.items()))
+        print(f"{n:6d} dispatches | {vals} | {name[:160]}")
+
+
+def load_traffic(workload: str, kernel: str) -> dict | None:
+    """HBM bytes per launch of the dominant kernel, measured by rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes and committed as profiles/traffic.json
+    (per workload and kernel, already scaled by the copy calibration)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        table = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    return table.get(workload, {}).get(kernel)
 
 
 def cpu_baseline(seconds: float) -> dict:
@@ -94,6 +133,9 @@ def cpu_baseline(seconds: float) -> dict:
 
 def main():
     args = parse()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
               "(the projection path runs on a single MI355X; multi-GPU sharding is a design "
@@ -195,6 +237,21 @@ def main():
             v["gbs"] = round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1)
             for key in ("ms", "flop", "bytes", "n"):
                 v.pop(key)
+
+    if roofline is not None:
+        kernel_id = roofline["kernel"]
+        t = load_traffic(args.workload, kernel_id)
+        if t is not None:
+            roofline["traffic"] = int(t["bytes_per_launch"])
+            roofline["traffic_source"] = t["source"]
+
+    if args.calibration_copy:
+        n = args.calibration_copy * (1 << 20) // 2
+        src = torch.ones(n, dtype=torch.bfloat16, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
 
     cpu = None
     if not args.no_cpu:

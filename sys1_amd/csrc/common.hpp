@@ -15,6 +15,7 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
+typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
 
 // Epilogue ids used as template arguments (a subset of flag combinations that
 // the dispatcher accepts; see epi_id_from_flags in the ABI source).

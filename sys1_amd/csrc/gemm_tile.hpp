@@ -319,7 +319,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
   // rounding, bias, gelu, gating) and go to the wave's LDS scratch as bf16,
   // row-major with 16-byte chunks rotated by row.  Phase 2: 8 lanes per row
   // read back 16-byte chunks, add the residual from 16-byte loads and store
-  // full 128-byte lines.
+  // full 128-byte lines.  Scratch is written and read through int vectors
+  // only, so type-based alias analysis cannot move one block's stores above
+  // the previous block's loads.
   constexpr int kOutCols = epi_gated(EPI) ? S::TN / 2 : S::TN;  // per wave
   constexpr int kC8 = kOutCols / 8;                             // 16-byte chunks per row
   static_assert(kOutCols % 8 == 0, "whole 16-byte chunks");
@@ -346,7 +348,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
             for (int e = 0; e < 4; ++e)
               o[e] = to_bf16(epi_gate<EPI>(acc[i][j][4 * g + e], acc[i][j][4 * (g + 2) + e]));
             const int col = i * 16 + 8 * g + nq;
-            *reinterpret_cast<bf16x4*>(sc_addr(frow, col / 8) + (col % 8) * 2) = o;
+            *reinterpret_cast<i32x2*>(sc_addr(frow, col / 8) + (col % 8) * 2) =
+                __builtin_bit_cast(i32x2, o);
           }
         } else {
 #pragma unroll
@@ -360,7 +363,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
             bf16x4 o;
 #pragma unroll
             for (int e = 0; e < 4; ++e) o[e] = to_bf16(epi_pre<EPI>(acc[i][j][4 * g + e], b[e]));
-            *reinterpret_cast<bf16x4*>(sc_addr(frow, col / 8) + (col % 8) * 2) = o;
+            *reinterpret_cast<i32x2*>(sc_addr(frow, col / 8) + (col % 8) * 2) =
+                __builtin_bit_cast(i32x2, o);
           }
         }
       }

@@ -77,21 +77,15 @@ constexpr KernelEntry tile_entry(const char* name, int occ, float eff) {
 // BN = 256, deep stages, K split over workgroups).
 const KernelEntry kKernels[] = {
     tile_entry<256, 256, 2, 4, 2, false>("tile_256x256_s2_w2x4", 1, 1.00f),
-    tile_entry<256, 160, 4, 1, 2, false>("tile_256x160_s2_w4x1", 1, 0.37f),
-    tile_entry<256, 128, 4, 2, 2, false>("tile_256x128_s2_w4x2", 1, 0.77f),
-    tile_entry<128, 256, 2, 4, 2, false>("tile_128x256_s2_w2x4", 1, 0.44f),
-    tile_entry<128, 192, 4, 2, 2, false>("tile_128x192_s2_w4x2", 1, 0.66f),
-    tile_entry<256, 96, 4, 1, 2, false>("tile_256x96_s2_w4x1", 1, 0.41f),
-    tile_entry<128, 128, 2, 2, 2, false>("tile_128x128_s2_w2x2", 2, 0.93f),
-    tile_entry<128, 64, 2, 1, 2, false>("tile_128x64_s2_w2x1", 2, 0.38f),
+    tile_entry<128, 256, 2, 4, 2, false>("tile_128x256_s2_w2x4", 1, 0.40f),
+    tile_entry<128, 192, 4, 2, 2, false>("tile_128x192_s2_w4x2", 1, 0.40f),
+    tile_entry<128, 128, 2, 2, 2, false>("tile_128x128_s2_w2x2", 2, 0.80f),
     tile_entry<32, 256, 1, 4, 4, true>("stream_32x256_s4_w1x4", 1, 0.50f),
     tile_entry<64, 256, 2, 4, 3, true>("stream_64x256_s3_w2x4", 1, 0.60f),
     tile_entry<128, 128, 2, 2, 2, true>("stream_128x128_s2_w2x2", 2, 0.90f),
     tile_entry<128, 256, 2, 4, 2, true>("stream_128x256_s2_w2x4", 1, 0.80f),
-    tile_entry<256, 128, 4, 2, 2, true>("stream_256x128_s2_w4x2", 1, 0.77f),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
-constexpr int kFirstStream = 8;
 
 int epi_id_from_flags(int32_t f) {
   switch (f) {
