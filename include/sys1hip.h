@@ -126,6 +126,12 @@ SYS1HIP_API int sys1hip_set_kernel(void* ctx, int32_t kernel_id);
  * ranges, clamped to the iteration count and to what the workspace holds. */
 SYS1HIP_API int sys1hip_set_grid(void* ctx, int32_t workgroups);
 
+/* Tuning and test knob, no counterpart in the reference: force how many
+ * tiles a stream-K kernel runs whole before its stream phase, for every
+ * later call on this context (-1 = automatic; clamped to the tile count).
+ * 0 is pure stream-K; the tile count is the plain tile schedule. */
+SYS1HIP_API int sys1hip_set_dp_tiles(void* ctx, int32_t tiles);
+
 /* Number of kernel ids and the name of one id (for sweeps). */
 SYS1HIP_API int sys1hip_kernel_count(void);
 SYS1HIP_API const char* sys1hip_kernel_name(int32_t kernel_id);

@@ -15,7 +15,6 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 typedef __attribute__((__vector_size__(4 * sizeof(int)))) int i32x4;
 typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
-typedef __attribute__((__vector_size__(2 * sizeof(int)))) int i32x2;
 
 // Epilogue ids used as template arguments (a subset of flag combinations that
 // the dispatcher accepts; see epi_id_from_flags in the ABI source).
@@ -109,6 +108,7 @@ struct GemmArgs {
   unsigned* counters;   // stream-K arrival counter per tile (zero between calls)
   int64_t ldx, ldw, ldr, ldy;
   int M, N, K, Nout;
+  int dp_tiles;         // stream-K kernels: tiles run whole before the stream phase
 };
 
 // Map the hardware workgroup id to a logical tile id so that each XCD gets a

@@ -4,19 +4,21 @@
 //   - small M (the weight-streaming regime): BM = the padded token count,
 //     BN = 256, with K split over workgroups so that every CU streams weight.
 //
-// Tile:    BM x BN output tile, BK = 64, WM x WN waves, each wave owns a
+// Tile:    BM x BN output tile, BK = 64 or 32, WM x WN waves, each wave owns a
 //          (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks.  The MFMA takes the
 //          weight block as A and the activation block as B, so a lane's
 //          accumulator holds runs of 4 consecutive output features of one
 //          token.
 // Loads:   global -> LDS directly (buffer_load ... lds, no VGPR staging).  One
-//          wave instruction fills 1 KB of LDS = 8 rows x 128 B; the 8 lanes
-//          of a row read its 128 B line (coalesced) in a permuted chunk order
-//          that realises the LDS swizzle below.  The x and w instructions of a
+//          wave instruction fills 1 KB of LDS = 8 rows x 128 B (BK = 64) or
+//          16 rows x 64 B (BK = 32); the lanes of a row read its line
+//          (coalesced) in a permuted chunk order that realises the LDS swizzle
+//          below.  The x and w instructions of a
 //          k-tile form one list dealt round-robin to the waves, so every wave
 //          issues the same count and vmcnt bookkeeping stays exact.
-// LDS:     per operand, row-major 128 B rows (64 bf16 of K); the 16-byte
-//          chunk c of row r sits at position c ^ f(r), f(r) = (r ^ r/8) & 7.
+// LDS:     per operand, row-major rows of BK bf16; the 16-byte chunk c of
+//          row r sits at position c ^ f(r), f(r) = (r ^ r/8) & 7 for 128 B
+//          rows ((r ^ r/4) & 3 for 64 B rows).
 //          With this f the MFMA operand reads (lanes 0-31: 32 rows of one
 //          chunk, lanes 32-63: the next chunk) run without LDS bank conflicts
 //          on gfx950 (SQ_LDS_BANK_CONFLICT = 0 measured; the plain r & 7 and
@@ -26,13 +28,16 @@
 //          loads overlap the current item's last k-tiles and its epilogue.
 //          Fragments are double-buffered in registers across k-steps, and the
 //          last k-step's MFMAs run after the barrier, overlapping the next
-//          k-tile's first LDS reads.
-// Epilogue: each wave transposes its output through a private LDS scratch
-//          block so that stores (and residual loads) move full 128-byte lines
-//          at 16 bytes per lane.
+//          k-tile's first LDS reads; the freed stage's refill is issued
+//          behind them.
+// Epilogue: straight from registers: lane pairs (l, l+32) exchange halves
+//          with v_permlane32_swap so that every lane stores (and reads the
+//          residual as) 16 contiguous bytes; no LDS, so all of it goes to
+//          pipeline stages.
 // Stream-K: the weight-streaming shapes split the flattened (tile, k-tile)
 //          iteration space into one equal contiguous range per workgroup, so
-//          every CU streams the same share of the weight.  A range covers at
+//          every CU streams the same share of the weight (optionally after a
+//          phase of whole tiles: the hybrid schedule of TileWalk).  A range covers at
 //          most a partial head segment, whole tiles, and a partial tail
 //          segment; a partial segment writes its f32 accumulators to the
 //          workspace (head or tail slot of its workgroup), and the last
@@ -75,28 +80,34 @@ __device__ __forceinline__ void vm_wait() {
 }
 
 // LDS row swizzle: chunk c of row r is stored at position c ^ swz(r).
-__device__ __forceinline__ int lds_swz(int row) { return (row ^ (row >> 3)) & 7; }
+// Measured conflict-free for the 32-lane fragment reads on gfx950: 128-byte
+// rows (BK = 64, 8 chunks) use (r ^ r/8) & 7, 64-byte rows (BK = 32, 4
+// chunks) use (r ^ r/4) & 3.
+template <int BK>
+__device__ __forceinline__ int lds_swz(int row) {
+  if constexpr (BK == 64) return (row ^ (row >> 3)) & 7;
+  else return (row ^ (row >> 2)) & 3;
+}
 
-template <int BM, int BN, int WM, int WN, int STAGES>
+template <int BM, int BN, int WM, int WN, int STAGES, int BK_>
 struct TileShape {
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = kWaves * 64;
-  static constexpr int BK = 64;
+  static constexpr int BK = BK_;
+  static_assert(BK == 32 || BK == 64, "k-tile of 32 or 64");
   static constexpr int TM = BM / WM;
   static constexpr int TN = BN / WN;
   static constexpr int FM = TM / 32;
   static constexpr int FN = TN / 32;
   static constexpr int KS = BK / 16;                 // MFMA k-steps per k-tile
-  static constexpr int kRowBytes = BK * 2;           // 128
-  static constexpr int RPI = 8;                      // rows per DMA instruction (1 KB)
+  static constexpr int kRowBytes = BK * 2;           // 128 or 64
+  static constexpr int CPR = BK / 8;                 // 16-byte chunks per row
+  static constexpr int RPI = 1024 / kRowBytes;       // rows per DMA instruction (1 KB)
   static constexpr int kXBytes = BM * kRowBytes;     // one stage of x
   static constexpr int kWBytes = BN * kRowBytes;
   static constexpr int kStageBytes = kXBytes + kWBytes;
   static constexpr int kStagesBytes = STAGES * kStageBytes;
-  // Epilogue scratch, private to each wave: one 32-row block of its output
-  // sub-tile in bf16.
-  static constexpr int kEpiBytes = 32 * TN * 2;
-  static constexpr int kLdsBytes = kStagesBytes + kWaves * kEpiBytes;
+  static constexpr int kLdsBytes = kStagesBytes;
   static constexpr int XT = BM / RPI;                // DMA instructions per k-tile: x
   static constexpr int DT = (BM + BN) / RPI;         // x and w together
   static constexpr int kDma = DT / kWaves;           // per wave per k-tile
@@ -112,57 +123,66 @@ struct TileShape {
 struct Segment {
   int tm, tn;     // tile coordinates
   int kt0, kt1;   // k-tile range
-  int pos;        // stream position of its first k-tile (tile * kt_count + kt0)
+  int pos;        // position in this workgroup's step sequence
+  int st;         // stream-phase tile index (tile - dp_tiles), -1 in the tile phase
+  int spos;       // stream-phase position of its first k-tile (st * kt_count + kt0)
 };
 
-// Persistent schedule.  The grid holds at most (CUs x resident workgroups
-// per CU) workgroups.
-//   Tile mode (large M): each segment is a whole tile.  Workgroup b serves
-//     XCD b % 8 and walks that XCD's contiguous share of the tiles with
-//     stride (workgroups on the XCD); tiles are rasterised in groups of
-//     kGroupM tile rows so the tiles in flight on one XCD share x row panels
-//     and w column panels in its L2.
-//   Stream mode (small M): workgroup g owns the flattened iterations
-//     [start(g), start(g+1)), start(g) = g * T / G, T = tiles * kt_count.
+// Persistent schedule over tiles rasterised in groups of kGroupM tile rows
+// (tiles in flight together share x row panels and w column panels in L2).
+// The grid holds at most (CUs x resident workgroups per CU) workgroups G.
+//   Tile phase: tiles [0, dp_tiles), each a whole segment.  Workgroup b
+//     serves XCD b % 8 and walks that XCD's contiguous share of these tiles
+//     with stride (workgroups on the XCD).
+//   Stream phase: the k-iterations of tiles [dp_tiles, tiles) flattened,
+//     T = (tiles - dp_tiles) * kt_count; workgroup g < G' = min(G, T) owns
+//     [start(g), start(g+1)), start(g) = g * T / G'.  A tile split over several
+//     workgroups is summed by its last arriving owner.
+// dp_tiles = tiles is the plain persistent tile schedule; dp_tiles = 0 is
+// pure stream-K (the weight-streaming small-M shapes); in between is the
+// hybrid that runs whole rounds of tiles and spreads the last, partial round
+// over every CU.
 struct TileWalk {
-  int tiles_m, tiles_n, kt_count;
-  bool stream;
-  // tile mode
+  int tiles_m, tiles_n, kt_count, tiles, dp_tiles;
+  // tile phase
   int first, count, stride;
-  // stream mode
+  // stream phase
   int64_t total;
-  int grid, begin, end;
+  int grid, sgrid, begin, end;  // sgrid: workgroups in the stream phase
+  int dp_steps;
 
   static constexpr int kGroupM = 4;
 
-  __device__ TileWalk(int M, int N, int K, int BM, int BN, int BK, bool streamk) {
+  __device__ TileWalk(int M, int N, int K, int BM, int BN, int BK, int dp) {
     tiles_m = (M + BM - 1) / BM;
     tiles_n = (N + BN - 1) / BN;
     kt_count = (K + BK - 1) / BK;
-    stream = streamk;
+    tiles = tiles_m * tiles_n;
+    dp_tiles = min(dp, tiles);
     grid = gridDim.x;
-    const int tiles = tiles_m * tiles_n;
-    if (stream) {
-      total = (int64_t)tiles * kt_count;
-      begin = start(blockIdx.x);
-      end = start(blockIdx.x + 1);
-      count = end > begin;
-    } else {
-      constexpr int kXcds = 8;
-      const int xcd = blockIdx.x % kXcds;
-      const int slot = blockIdx.x / kXcds;
-      const int slots = grid / kXcds + (xcd < grid % kXcds ? 1 : 0);  // workgroups on this XCD
-      const int per = tiles / kXcds, rem = tiles % kXcds;
-      const int xbegin = xcd * per + min(xcd, rem);
-      const int xcount = per + (xcd < rem ? 1 : 0);
-      first = xbegin + slot;
-      stride = slots;
-      count = slot < xcount ? (xcount - slot + slots - 1) / slots : 0;
-    }
+    // Workgroups are dispatched round-robin over the 8 XCDs; a grid smaller
+    // than that deals the tiles over as many groups as it has workgroups.
+    const int xcds = min(8, grid);
+    const int xcd = blockIdx.x % xcds;
+    const int slot = blockIdx.x / xcds;
+    const int slots = grid / xcds + (xcd < grid % xcds ? 1 : 0);  // workgroups on this XCD
+    const int per = dp_tiles / xcds, rem = dp_tiles % xcds;
+    const int xbegin = xcd * per + min(xcd, rem);
+    const int xcount = per + (xcd < rem ? 1 : 0);
+    first = xbegin + slot;
+    stride = slots;
+    count = slot < xcount ? (xcount - slot + slots - 1) / slots : 0;
+    dp_steps = count * kt_count;
+    total = (int64_t)(tiles - dp_tiles) * kt_count;
+    // At most one workgroup per iteration, so that every stream range is
+    // non-empty (the arrival count of a split tile is its owner count).
+    sgrid = (int)min<int64_t>(grid, total);
+    begin = (int)blockIdx.x < sgrid ? start(blockIdx.x) : 0;
+    end = (int)blockIdx.x < sgrid ? start(blockIdx.x + 1) : 0;
   }
-  __device__ int start(int g) const { return (int)((int64_t)g * total / grid); }
+  __device__ int start(int g) const { return (int)((int64_t)g * total / sgrid); }
 
-  // Tile-mode tile index j of this workgroup -> coordinates (grouped raster).
+  // Tile index -> coordinates (grouped raster).
   __device__ void tile_coords(int t, int& tm, int& tn) const {
     const int group = t / (kGroupM * tiles_n);
     const int first_m = group * kGroupM;
@@ -171,41 +191,42 @@ struct TileWalk {
     tm = first_m + in % gm;
     tn = in / gm;
   }
-  __device__ int steps() const {
-    return stream ? end - begin : count * kt_count;
-  }
-  // Segment starting at stream position `pos` (stream mode) or at tile-mode
-  // index j = pos / kt_count.
+  __device__ int steps() const { return dp_steps + (end - begin); }
+  // The segment whose first k-tile is step `pos` of this workgroup.
   __device__ Segment segment_at(int pos) const {
     Segment sg;
-    if (stream) {
-      const int t = pos / kt_count;
-      sg.tm = t / tiles_n;
-      sg.tn = t - sg.tm * tiles_n;
-      sg.kt0 = pos - t * kt_count;
-      sg.kt1 = min(kt_count, sg.kt0 + (end - pos));
-    } else {
+    if (pos < dp_steps) {
       const int j = pos / kt_count;
       tile_coords(first + j * stride, sg.tm, sg.tn);
       sg.kt0 = 0;
       sg.kt1 = kt_count;
+      sg.st = -1;
+      sg.spos = 0;
+    } else {
+      const int sp = begin + (pos - dp_steps);
+      const int t = sp / kt_count;
+      tile_coords(dp_tiles + t, sg.tm, sg.tn);
+      sg.kt0 = sp - t * kt_count;
+      sg.kt1 = min(kt_count, sg.kt0 + (end - sp));
+      sg.st = t;
+      sg.spos = sp;
     }
     sg.pos = pos;
     return sg;
   }
-  __device__ Segment first_segment() const { return segment_at(stream ? begin : 0); }
+  __device__ Segment first_segment() const { return segment_at(0); }
   __device__ Segment next_segment(const Segment& sg) const {
     return segment_at(sg.pos + (sg.kt1 - sg.kt0));
   }
   __device__ bool complete(const Segment& sg) const { return sg.kt0 == 0 && sg.kt1 == kt_count; }
-  // Stream mode: the workgroups whose ranges overlap tile t, [g_lo, g_hi].
-  __device__ void tile_owners(int t, int& g_lo, int& g_hi) const {
-    const int64_t lo = (int64_t)t * kt_count, hi = lo + kt_count;  // [lo, hi)
-    int g = (int)(lo * grid / total);
+  // Stream phase: the workgroups whose ranges overlap stream tile st, [g_lo, g_hi].
+  __device__ void tile_owners(int st, int& g_lo, int& g_hi) const {
+    const int64_t lo = (int64_t)st * kt_count, hi = lo + kt_count;  // [lo, hi)
+    int g = (int)(lo * sgrid / total);
     while (g > 0 && start(g) > lo) --g;
     while (start(g + 1) <= lo) ++g;
     g_lo = g;
-    g = (int)((hi - 1) * grid / total);
+    g = (int)((hi - 1) * sgrid / total);
     while (g > 0 && start(g) > hi - 1) --g;
     while (start(g + 1) <= hi - 1) ++g;
     g_hi = g;
@@ -214,14 +235,16 @@ struct TileWalk {
 
 // STREAMK: stream-K schedule (the weight-streaming shapes); the large-M
 // shapes compile the tile schedule only.
-template <int BM, int BN, int WM, int WN, int STAGES, bool STREAMK, int EPI>
+template <int BM, int BN, int WM, int WN, int STAGES, int BK_, bool STREAMK, int EPI>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
-  using S = TileShape<BM, BN, WM, WN, STAGES>;
+  using S = TileShape<BM, BN, WM, WN, STAGES, BK_>;
   constexpr int BK = S::BK;
   __shared__ __attribute__((aligned(1024))) char lds[S::kLdsBytes];
+  __shared__ int arrival_flag;  // stream-K: the tile's last owner
+  static_assert(!STREAMK || S::kLdsBytes + 16 <= 160 * 1024, "LDS budget with the arrival flag");
 
-  const TileWalk walk(a.M, a.N, a.K, BM, BN, BK, STREAMK);
-  if (walk.count == 0) return;
+  const TileWalk walk(a.M, a.N, a.K, BM, BN, BK, STREAMK ? a.dp_tiles : 1 << 30);
+  if (walk.steps() == 0) return;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -231,34 +254,59 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
 
   // ---- DMA.  The issue cursor walks the segments in stream order.
   // Instruction u = i * waves + wave of a k-tile: u < XT covers x rows
-  // 8u .. 8u+7, else w rows 8(u-XT) ..; either way its 1 KB lands at stage
-  // offset u * 1 KB.  Lane -> row + lane/8, position lane%8, source chunk
-  // position ^ swz(row).  Rows past M / N clamp to the last row; chunks past
-  // K read zeros through an out-of-range buffer offset.
-  const int lrow = lane >> 3, lpos = lane & 7;
+  // RPI*u .. RPI*u + RPI-1, else w rows RPI*(u-XT) ..; either way its 1 KB
+  // lands at stage offset u * 1 KB.  Lane -> row + lane/CPR, position
+  // lane%CPR, source chunk position ^ swz(row).  Rows past M / N clamp to
+  // the last row; chunks past K read zeros through an out-of-range buffer
+  // offset.
+  const int lrow = lane / S::CPR, lpos = lane % S::CPR;
+  // A wave's first kXDma instructions read x, the rest w.  Row, chunk and
+  // swizzle of each instruction depend only on the lane, so the per-lane
+  // source offsets (row clamp included) are computed when the issue cursor
+  // enters a tile; a k-tile then costs only the scalar base advance, and the
+  // K-tail test runs on a tile's last, partial k-tile only.
+  static_assert(S::XT % S::kWaves == 0, "x and w instructions split evenly per wave");
+  constexpr int kXDma = S::XT / S::kWaves;
+  auto dma_row = [&](int i) {
+    const int u = i * S::kWaves + wave;
+    return (i < kXDma ? u : u - S::XT) * S::RPI + lrow;
+  };
+  unsigned src_off[S::kDma];
+  auto set_offsets = [&](const Segment& sg) {
+    const int x_left = a.M - 1 - sg.tm * BM, w_left = a.N - 1 - sg.tn * BN;
+#pragma unroll
+    for (int i = 0; i < S::kDma; ++i) {
+      const int r = dma_row(i);
+      const int c = lpos ^ lds_swz<BK>(r);
+      src_off[i] = i < kXDma ? (unsigned)(min(r, x_left) * (int)a.ldx * 2 + c * 16)
+                             : (unsigned)(min(r, w_left) * (int)a.ldw * 2 + c * 16);
+    }
+  };
   Segment isg = walk.first_segment();
   int is_kt = isg.kt0;
+  set_offsets(isg);
   auto issue = [&](int stage) {  // issue the cursor's k-tile, then advance the cursor
     const int m0 = isg.tm * BM, n0 = isg.tn * BN;
     char* base = lds + stage * S::kStageBytes;
     const rsrc_t xr = make_rsrc(reinterpret_cast<const char*>(a.x + (int64_t)m0 * a.ldx) + is_kt * BK * 2);
     const rsrc_t wr = make_rsrc(reinterpret_cast<const char*>(a.w + (int64_t)n0 * a.ldw) + is_kt * BK * 2);
     const int kleft = a.K - is_kt * BK;  // valid K elements in this k-tile
+    if (kleft >= BK) {
 #pragma unroll
-    for (int i = 0; i < S::kDma; ++i) {
-      const int u = i * S::kWaves + wave;
-      const bool is_x = u < S::XT;
-      const int r = (is_x ? u : u - S::XT) * S::RPI + lrow;
-      const int c = lpos ^ lds_swz(r);
-      const int rows_left = is_x ? a.M - 1 - m0 : a.N - 1 - n0;
-      const int ld = is_x ? (int)a.ldx : (int)a.ldw;
-      unsigned off = (unsigned)(min(r, rows_left) * ld * 2 + c * 16);
-      if (c * 8 >= kleft) off = kOutOfRange;
-      dma16(is_x ? xr : wr, off, (lds_void*)(base + u * 1024));
+      for (int i = 0; i < S::kDma; ++i)
+        dma16(i < kXDma ? xr : wr, src_off[i], (lds_void*)(base + (i * S::kWaves + wave) * 1024));
+    } else {
+#pragma unroll
+      for (int i = 0; i < S::kDma; ++i) {
+        const int c = lpos ^ lds_swz<BK>(dma_row(i));
+        const unsigned off = c * 8 >= kleft ? kOutOfRange : src_off[i];
+        dma16(i < kXDma ? xr : wr, off, (lds_void*)(base + (i * S::kWaves + wave) * 1024));
+      }
     }
     if (++is_kt == isg.kt1) {
       isg = walk.next_segment(isg);
       is_kt = isg.kt0;
+      set_offsets(isg);
     }
   };
 
@@ -271,13 +319,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
   for (int j = 0; j < S::FM; ++j) {
     const int r = wm * S::TM + j * 32 + frow;
     xrow_off[j] = r * S::kRowBytes;
-    xrow_swz[j] = lds_swz(r);
+    xrow_swz[j] = lds_swz<BK>(r);
   }
 #pragma unroll
   for (int i = 0; i < S::FN; ++i) {
     const int r = wn * S::TN + i * 32 + frow;
     wrow_off[i] = S::kXBytes + r * S::kRowBytes;
-    wrow_swz[i] = lds_swz(r);
+    wrow_swz[i] = lds_swz<BK>(r);
   }
 
   struct Frags {
@@ -313,81 +361,72 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
       for (int j = 0; j < S::FM; ++j) acc[i][j] = mfma32(f.w[i], f.x[j], acc[i][j]);
   };
 
-  // ---- epilogue of one tile, one 32-row block at a time.  Phase 1: the
-  // lane's accumulators (token m = lane%32 of the block, features
-  // 8g + 4*(lane/32) + [0..3]) get the register-side epilogue ops (bf16
-  // rounding, bias, gelu, gating) and go to the wave's LDS scratch as bf16,
-  // row-major with 16-byte chunks rotated by row.  Phase 2: 8 lanes per row
-  // read back 16-byte chunks, add the residual from 16-byte loads and store
-  // full 128-byte lines.  Scratch is written and read through int vectors
-  // only, so type-based alias analysis cannot move one block's stores above
-  // the previous block's loads.
-  constexpr int kOutCols = epi_gated(EPI) ? S::TN / 2 : S::TN;  // per wave
-  constexpr int kC8 = kOutCols / 8;                             // 16-byte chunks per row
-  static_assert(kOutCols % 8 == 0, "whole 16-byte chunks");
-  char* scratch = lds + S::kStagesBytes + wave * S::kEpiBytes;
-  auto sc_addr = [&](int row, int c8) -> char* {
-    return scratch + row * (kOutCols * 2) + ((c8 + row) % kC8) * 16;
+  // ---- epilogue of one tile, straight from registers.  A lane's
+  // accumulator block (i, j) holds token m = lane%32 and, in register
+  // 4g + e, feature 8g + 4h + e (h = lane/32).  For a register-group pair
+  // (g, g+1), lanes l and l+32 hold the two 8-byte halves of token l's
+  // features 8g .. 8g+7 and 8(g+1) .. 8(g+1)+7 crosswise; one
+  // v_permlane32_swap per dword turns that into 16 contiguous bytes per lane
+  // (lane l: features 8g.., lane l+32: 8(g+1)..), stored with one 16-byte
+  // store.  Rounding mirrors the unfused reference: the projection (or the
+  // gated product) is rounded to bf16 in registers; bias, gelu and the
+  // residual add then apply in f32 on the stored layout, each rounded.
+  auto pair16 = [](bf16x4 lo, bf16x4 hi) -> bf16x8 {
+    const i32x2 a = __builtin_bit_cast(i32x2, lo), b = __builtin_bit_cast(i32x2, hi);
+    const auto s0 = __builtin_amdgcn_permlane32_swap((unsigned)a[0], (unsigned)b[0], false, false);
+    const auto s1 = __builtin_amdgcn_permlane32_swap((unsigned)a[1], (unsigned)b[1], false, false);
+    const i32x4 v = {(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
+    return __builtin_bit_cast(bf16x8, v);
   };
   auto epilogue = [&](int m0, int n0) {
-    const int nq = 4 * fk;
-    const int out_n0 = (epi_gated(EPI) ? (n0 + wn * S::TN) / 2 : n0 + wn * S::TN);
+    const int h = fk;
+    const int out_n0 = epi_gated(EPI) ? (n0 + wn * S::TN) / 2 : n0 + wn * S::TN;
 #pragma unroll
     for (int j = 0; j < S::FM; ++j) {
-      // phase 1: registers -> scratch
+      const int m = m0 + wm * S::TM + j * 32 + frow;
+      const bool row_ok = m < a.M;
 #pragma unroll
       for (int i = 0; i < S::FN; ++i) {
         if constexpr (epi_gated(EPI)) {
           // A 32-row block of the packed weight is 16 gate rows then the 16
           // up rows of the same 16 output columns: registers 4g+e (g = 0, 1)
           // hold gate rows, 4(g+2)+e the matching up rows.
+          bf16x4 o[2];
 #pragma unroll
-          for (int g = 0; g < 2; ++g) {
-            bf16x4 o;
+          for (int g = 0; g < 2; ++g)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              o[e] = to_bf16(epi_gate<EPI>(acc[i][j][4 * g + e], acc[i][j][4 * (g + 2) + e]));
-            const int col = i * 16 + 8 * g + nq;
-            *reinterpret_cast<i32x2*>(sc_addr(frow, col / 8) + (col % 8) * 2) =
-                __builtin_bit_cast(i32x2, o);
-          }
+              o[g][e] = to_bf16(epi_gate<EPI>(acc[i][j][4 * g + e], acc[i][j][4 * (g + 2) + e]));
+          const bf16x8 v = pair16(o[0], o[1]);
+          const int n = out_n0 + i * 16 + 8 * h;
+          if (row_ok && n < a.Nout) store8(a.y + (int64_t)m * a.ldy + n, v, a.Nout - n);
         } else {
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int col = i * 32 + 8 * g + nq;
-            float b[4] = {0, 0, 0, 0};
-            if constexpr (epi_has_bias<EPI>()) {
-              const int n = n0 + wn * S::TN + col;
-              load4(a.bias + n, b, a.Nout - n);
+          for (int gp = 0; gp < 2; ++gp) {
+            bf16x4 p[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) p[q][e] = to_bf16(acc[i][j][4 * (2 * gp + q) + e]);
+            bf16x8 v = pair16(p[0], p[1]);
+            const int n = out_n0 + i * 32 + 16 * gp + 8 * h;
+            if (row_ok && n < a.Nout) {
+              const int valid = a.Nout - n;
+              if constexpr (EPI != kEpiNone) {
+                float b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                if constexpr (epi_has_bias<EPI>()) load8(a.bias + n, b, valid);
+                float r[8];
+                if constexpr (epi_has_resid<EPI>()) load8(a.resid + (int64_t)m * a.ldr + n, r, valid);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                  float t = epi_pre<EPI>(to_f32(v[e]), b[e]);
+                  if constexpr (epi_has_resid<EPI>()) t = round_bf16(t + r[e]);
+                  v[e] = to_bf16(t);
+                }
+              }
+              store8(a.y + (int64_t)m * a.ldy + n, v, valid);
             }
-            bf16x4 o;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = to_bf16(epi_pre<EPI>(acc[i][j][4 * g + e], b[e]));
-            *reinterpret_cast<i32x2*>(sc_addr(frow, col / 8) + (col % 8) * 2) =
-                __builtin_bit_cast(i32x2, o);
           }
-        }
-      }
-      // phase 2: scratch -> global, 16 bytes per lane
-      const int mb = m0 + wm * S::TM + j * 32;
-#pragma unroll
-      for (int t = 0; t < (32 * kC8 + 63) / 64; ++t) {
-        const int q = lane + 64 * t;
-        if (32 * kC8 % 64 != 0 && q >= 32 * kC8) break;
-        const int row = q / kC8, c8 = q % kC8;
-        const int m = mb + row;
-        const int n = out_n0 + c8 * 8;
-        const i32x4 raw = *reinterpret_cast<const i32x4*>(sc_addr(row, c8));
-        if (m < a.M && n < a.Nout) {
-          const int valid = a.Nout - n;
-          bf16x8 v = __builtin_bit_cast(bf16x8, raw);
-          if constexpr (epi_has_resid<EPI>()) {
-            float r[8];
-            load8(a.resid + (int64_t)m * a.ldr + n, r, valid);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = to_bf16(to_f32(v[e]) + r[e]);
-          }
-          store8(a.y + (int64_t)m * a.ldy + n, v, valid);
         }
       }
     }
@@ -413,8 +452,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
   // is the tile's last segment to arrive, with acc then holding the full sum
   // (the caller runs the epilogue).
   auto finish_partial = [&](const Segment& sg) -> bool {
-    const int t = sg.tm * walk.tiles_n + sg.tn;
-    const int slot = sg.pos == walk.begin ? 0 : 1;
+    const int t = sg.st;
+    const int slot = sg.spos == walk.begin ? 0 : 1;
     const unsigned mine = slot_off(blockIdx.x, slot);
     // (sched_barrier keeps the scheduler from hoisting the whole partial's
     // memory traffic together: that would raise the register peak of the
@@ -437,10 +476,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
     walk.tile_owners(t, g_lo, g_hi);
     __builtin_amdgcn_s_waitcnt(0);  // every wave: its partial stores are acknowledged
     __syncthreads();
-    // The arrival result goes through the first word of wave 0's epilogue
-    // scratch (free here: every wave has finished its previous epilogue),
-    // with a second barrier before anyone may overwrite it.
-    volatile int* flag = reinterpret_cast<volatile int*>(lds + S::kStagesBytes);
+    // The arrival result goes through an LDS word, with a second barrier
+    // before the next partial may overwrite it.
+    volatile int* flag = &arrival_flag;
     if (tid == 0) {
       const unsigned prev = __hip_atomic_fetch_add(a.counters + t, 1u, __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT);
@@ -493,33 +531,40 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
 
   Segment csg = walk.first_segment();  // compute cursor
   int ckt = csg.kt0;
-  Frags f0, f1;
-  if (steps > 0) read(f0, 0, 0);
+  Frags fr[2];  // ping-pong fragment sets: k-step ks reads into fr[ks % 2]
+  if (steps > 0) read(fr[0], 0, 0);
   int stage = 0;
   for (int s = 0; s < steps; ++s) {
+    // The k-tile's first fragments (read before the previous k-tile's last
+    // MFMAs) are in.  Waiting for them here, explicitly, keeps the compiler
+    // from resolving its merged loop-header state with a full LDS wait placed
+    // after the next fragment reads, which would serialise LDS latency with
+    // every k-tile's first MFMAs.
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt unconstrained
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int ks = 1; ks < S::KS; ks += 2) {
-      read(f1, stage, ks);
+    for (int ks = 1; ks < S::KS; ++ks) {
+      read(fr[ks % 2], stage, ks);
       __builtin_amdgcn_sched_barrier(0);
-      mma(f0);
+      mma(fr[(ks - 1) % 2]);
       __builtin_amdgcn_sched_barrier(0);
-      if (ks + 1 < S::KS) {
-        read(f0, stage, ks + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        mma(f1);
-        __builtin_amdgcn_sched_barrier(0);
-      }
     }
     if (s + 1 < steps) {
       if (s + STAGES - 1 < steps) vm_wait<(STAGES - 2) * S::kDma>();
       else vm_wait<0>();
     }
     __syncthreads();
-    if (s + STAGES < steps) issue(stage);
+    // Next k-tile's first fragments, this k-tile's last MFMAs, then the
+    // refill of the stage just freed: the refill's load instructions can
+    // stall issue while the load path drains, and issued behind the MFMAs
+    // that stall overlaps matrix work instead of delaying it.
+    const int freed = stage;
     stage = stage + 1 == STAGES ? 0 : stage + 1;
-    if (s + 1 < steps) read(f0, stage, 0);
+    if (s + 1 < steps) read(fr[0], stage, 0);
     __builtin_amdgcn_sched_barrier(0);
-    mma(f1);
+    mma(fr[(S::KS - 1) % 2]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + STAGES < steps) issue(freed);
     __builtin_amdgcn_sched_barrier(0);
     if (++ckt == csg.kt1) {
       if constexpr (STREAMK) {

@@ -48,6 +48,7 @@ struct Context {
   unsigned* counters = nullptr;
   int forced_kernel = -1;
   int forced_grid = 0;
+  int forced_dp = -1;
   int cus = 256;
 };
 
@@ -60,30 +61,31 @@ struct KernelEntry {
   bool streamk;         // stream-K schedule (weight-streaming shapes)
   float efficiency;     // measured MFMA efficiency of the shape, fitted to a sweep of the
                         // projection shapes (ModernBERT base/large, Qwen, square)
+  int bk;               // k-tile depth
   KernelFn fn[kEpiCount];
 };
 
-template <int BM, int BN, int WM, int WN, int ST, bool SK>
+template <int BM, int BN, int WM, int WN, int ST, int BK, bool SK>
 constexpr KernelEntry tile_entry(const char* name, int occ, float eff) {
-  return KernelEntry{name, BM, BN, WM * WN * 64, occ, SK, eff,
-                     {gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 0>, gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 1>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 2>, gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 3>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 4>, gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 5>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, SK, 6>}};
+  return KernelEntry{name, BM, BN, WM * WN * 64, occ, SK, eff, BK,
+                     {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 0>, gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 1>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 2>, gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 3>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 4>, gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 5>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 6>}};
 }
 
 // Output-tile shapes.  The first group serves large M (MFMA-bound); the
 // "stream" group serves small M (weight-streaming: BM = padded token count,
 // BN = 256, deep stages, K split over workgroups).
 const KernelEntry kKernels[] = {
-    tile_entry<256, 256, 2, 4, 2, false>("tile_256x256_s2_w2x4", 1, 1.00f),
-    tile_entry<128, 256, 2, 4, 2, false>("tile_128x256_s2_w2x4", 1, 0.40f),
-    tile_entry<128, 192, 4, 2, 2, false>("tile_128x192_s2_w4x2", 1, 0.40f),
-    tile_entry<128, 128, 2, 2, 2, false>("tile_128x128_s2_w2x2", 2, 0.80f),
-    tile_entry<32, 256, 1, 4, 4, true>("stream_32x256_s4_w1x4", 1, 0.50f),
-    tile_entry<64, 256, 2, 4, 3, true>("stream_64x256_s3_w2x4", 1, 0.60f),
-    tile_entry<128, 128, 2, 2, 2, true>("stream_128x128_s2_w2x2", 2, 0.90f),
-    tile_entry<128, 256, 2, 4, 2, true>("stream_128x256_s2_w2x4", 1, 0.80f),
+    tile_entry<256, 256, 2, 4, 2, 64, false>("tile_256x256_s2_w2x4", 1, 1.00f),
+    tile_entry<128, 256, 2, 4, 2, 64, false>("tile_128x256_s2_w2x4", 1, 0.40f),
+    tile_entry<128, 192, 4, 2, 2, 64, false>("tile_128x192_s2_w4x2", 1, 0.40f),
+    tile_entry<128, 128, 2, 2, 2, 64, false>("tile_128x128_s2_w2x2", 2, 0.80f),
+    tile_entry<32, 256, 1, 4, 4, 64, true>("stream_32x256_s4_w1x4", 1, 0.50f),
+    tile_entry<64, 256, 2, 4, 3, 64, true>("stream_64x256_s3_w2x4", 1, 0.60f),
+    tile_entry<128, 128, 2, 2, 2, 64, true>("stream_128x128_s2_w2x2", 2, 0.80f),
+    tile_entry<128, 256, 2, 4, 2, 64, true>("stream_128x256_s2_w2x4", 1, 0.80f),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
@@ -103,39 +105,50 @@ int epi_id_from_flags(int32_t f) {
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Modelled time (in CU clocks) of a projection on kernel `e` launched on
-// `grid` workgroups.  Tile shapes: (tile rounds over the resident slots) x
-// (per-tile cycles).  Stream-K shapes: the iteration space divided evenly
-// over the grid, plus the partial-tile fix-up traffic and latency.  A tile's
-// cycles are the larger of its MFMA cycles (derated by the shape's measured
-// efficiency) and its operand loads at about 48 B/clk per CU from L2, plus
-// its output write; the whole call is bounded below by the chip's HBM time
-// for the weights.
+// `grid` workgroups, of which the first `dp` tiles run whole (tile phase)
+// and the rest are split over every workgroup (stream phase; stream-K
+// kernels only).  A tile's cycles per k-tile are the larger of its MFMA
+// cycles (derated by the shape's measured efficiency) and its operand loads
+// at about 48 B/clk per CU from L2; workgroups sharing a CU share its time.
+// A split tile costs its last arriving owner the arrival latency plus
+// reading every owner's f32 partial.  The whole call is bounded below by the
+// chip's HBM time for the weights.
 constexpr double kFlopPerClk = 4096.0;      // bf16 MFMA per CU per clock
 constexpr double kLoadBytesPerClk = 48.0;   // L2 -> CU
 constexpr double kStoreBytesPerClk = 64.0;
 constexpr double kHbmBytesPerClk = 3000.0;  // ~6.6 TB/s sustained at ~2.2 GHz, whole chip
-constexpr double kFixupClk = 6000.0;        // partial write + arrival + reduction latency
+constexpr double kFixupClk = 6000.0;        // partial write + arrival latency
+
+struct Plan {
+  int kernel = 0;
+  int64_t grid = 1;
+  int64_t dp = 0;  // tiles run whole before the stream phase (stream-K kernels)
+  double cost = 1e300;
+};
 
 double model_cost(const Context* c, const KernelEntry& e, int64_t M, int64_t N, int64_t K,
-                  int64_t grid) {
+                  int64_t grid, int64_t dp) {
   const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
-  const int64_t kts = cdiv(K, 64);
-  const double mfma = 2.0 * e.bm * e.bn * 64.0 / kFlopPerClk / e.efficiency;  // per k-tile
-  const double load = (double)(e.bm + e.bn) * 64.0 * 2.0 / kLoadBytesPerClk;
+  const int64_t kts = cdiv(K, e.bk);
+  const double mfma = 2.0 * e.bm * e.bn * e.bk / kFlopPerClk / e.efficiency;  // per k-tile
+  const double load = (double)(e.bm + e.bn) * e.bk * 2.0 / kLoadBytesPerClk;
   const double per_kt = std::max(mfma, load);
   const double store = 2.0 * e.bm * e.bn / kStoreBytesPerClk;
   const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk;
-  double t;
-  if (e.streamk) {
-    const double iters = (double)cdiv(tiles * kts, grid);
-    const double tiles_per_wg = (double)cdiv(tiles, grid) + 1.0;
-    const bool partial = grid > tiles || (tiles * kts) % grid != 0;
-    t = iters * per_kt + tiles_per_wg * store + (partial ? kFixupClk : 0.0);
-    const double fix = partial ? 2.0 * 2.0 * grid * e.bm * e.bn * 4.0 / kHbmBytesPerClk : 0.0;
-    return std::max(t, hbm) + fix;
+  const double share = std::max(1.0, (double)grid / c->cus);  // workgroups per CU
+  double t = (double)cdiv(dp, grid) * share * (kts * per_kt + store);
+  const int64_t st = tiles - dp;
+  if (st > 0) {
+    const int64_t total = st * kts;
+    const int64_t sg = std::min(grid, total);  // workgroups in the stream phase
+    const double iters = (double)cdiv(total, sg);
+    t += share * (iters * per_kt + ((double)cdiv(st, sg) + 1.0) * store);
+    if (total % sg != 0 || sg > st) {
+      const double owners = std::min<double>((double)sg, (double)sg / st + 1.0);
+      t += kFixupClk + owners * e.bm * e.bn * 4.0 / kLoadBytesPerClk;
+      t += 2.0 * 2.0 * sg * e.bm * e.bn * 4.0 / kHbmBytesPerClk;  // partial traffic
+    }
   }
-  const int64_t rounds = cdiv(tiles, (int64_t)c->cus * e.occupancy) * e.occupancy;
-  t = (double)rounds * (kts * per_kt + store);
   return std::max(t, hbm);
 }
 
@@ -143,43 +156,64 @@ int64_t max_grid(const Context* c, const KernelEntry& e, int64_t M, int64_t N, i
   const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
   int64_t g = (int64_t)c->cus * e.occupancy;
   if (!e.streamk) return std::min(g, tiles);
-  g = std::min(g, tiles * cdiv(K, 64));
+  g = std::min(g, tiles * cdiv(K, e.bk));
   while (g > 1 && 2 * g * e.bm * e.bn * 4 > (int64_t)kWorkspaceBytes) --g;
   return g;
 }
 
-// Automatic choice of kernel and grid: the lowest modelled time over the
-// shapes that fit M (stream shapes only for M up to their BM; tile shapes
-// only above 128 tokens).  Stream-K grids from a quarter of the CUs up to all
-// of them are tried.
-void choose(const Context* c, int64_t M, int64_t N, int64_t K, int* kernel, int* grid) {
-  double best = 1e300;
-  *kernel = 0;
-  *grid = 1;
-  for (int id = 0; id < kNumKernels; ++id) {
-    const KernelEntry& e = kKernels[id];
-    if (e.streamk && M > e.bm) continue;
-    if (!e.streamk && M <= 128) continue;
-    const int64_t gmax = max_grid(c, e, M, N, K);
-    const int64_t gmin = e.streamk ? std::max<int64_t>(1, gmax / 4) : gmax;
-    for (int64_t g = gmax; g >= gmin; g -= std::max<int64_t>(1, gmax / 16)) {
-      const double cost = model_cost(c, e, M, N, K, g);
-      if (cost < best * 0.999) best = cost, *kernel = id, *grid = (int)g;
+// Prices kernel `id` on `grid` workgroups and keeps it in *best when it is
+// cheaper.  Tile kernels run every tile whole.  Stream-K kernels try: pure
+// stream-K, the hybrid whose stream phase is the last partial round of
+// tiles, and the hybrid whose stream phase also takes one full round (more
+// iterations per workgroup, fewer owners per split tile).
+void consider(const Context* c, int id, int64_t M, int64_t N, int64_t K, int64_t grid, Plan* best) {
+  const KernelEntry& e = kKernels[id];
+  const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
+  int64_t cand[3] = {tiles, -1, -1};
+  if (e.streamk && c->forced_dp >= 0) {
+    cand[0] = std::min<int64_t>(c->forced_dp, tiles);
+  } else if (e.streamk) {
+    const int64_t whole = tiles / grid * grid;
+    cand[0] = 0;
+    if (whole > 0 && whole < tiles) cand[1] = whole;
+    if (whole > grid && whole < tiles) cand[2] = whole - grid;
+    if (whole == tiles) cand[1] = tiles;
+  }
+  for (int64_t dp : cand) {
+    if (dp < 0 || tiles - dp > kCounterSlots) continue;
+    const double cost = model_cost(c, e, M, N, K, grid, dp);
+    if (cost < best->cost * 0.999) {
+      best->kernel = id, best->grid = grid, best->dp = dp, best->cost = cost;
     }
   }
 }
 
-// Kernel and grid for a call: the automatic choice, or a forced kernel id
-// and/or a forced grid size.
-void resolve(const Context* c, int64_t M, int64_t N, int64_t K, int* kernel, int* grid) {
-  if (c->forced_kernel < 0) {
-    choose(c, M, N, K, kernel, grid);
-  } else {
-    *kernel = c->forced_kernel;
-    *grid = (int)max_grid(c, kKernels[*kernel], M, N, K);
+// Plan of a call: the cheapest modelled (kernel, grid, dp) over the shapes
+// allowed for M (stream-K shapes where M fits their tile height, tile shapes
+// above 128 tokens), or over the forced kernel, grid and/or dp.  Stream-K grids from a quarter of
+// the slots up to all of them are tried.
+Plan resolve(const Context* c, int64_t M, int64_t N, int64_t K) {
+  Plan best;
+  for (int id = 0; id < kNumKernels; ++id) {
+    if (c->forced_kernel >= 0 && id != c->forced_kernel) continue;
+    const KernelEntry& e = kKernels[id];
+    if (c->forced_kernel < 0) {
+      // Measured in the projection chains: the large-M hybrid loses to the
+      // plain tile schedule (every split tile moves two f32 partials across
+      // the fabric), so stream-K is chosen only where M fits one tile row.
+      if (e.streamk && M > e.bm) continue;
+      if (!e.streamk && M <= 128) continue;
+    }
+    const int64_t gmax = max_grid(c, e, M, N, K);
+    if (c->forced_grid > 0) {
+      consider(c, id, M, N, K, std::min<int64_t>(c->forced_grid, gmax), &best);
+      continue;
+    }
+    const int64_t gmin = e.streamk && M <= e.bm ? std::max<int64_t>(1, gmax / 4) : gmax;
+    for (int64_t g = gmax; g >= gmin; g -= std::max<int64_t>(1, gmax / 16))
+      consider(c, id, M, N, K, g, &best);
   }
-  if (c->forced_grid > 0)
-    *grid = (int)std::min<int64_t>(c->forced_grid, max_grid(c, kKernels[*kernel], M, N, K));
+  return best;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -298,6 +332,13 @@ int sys1hip_set_grid(void* ctx, int32_t workgroups) {
   return SYS1HIP_OK;
 }
 
+int sys1hip_set_dp_tiles(void* ctx, int32_t tiles) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_set_dp_tiles: null context");
+  if (tiles < -1) return fail(SYS1HIP_EINVAL, "sys1hip_set_dp_tiles: %d below -1", tiles);
+  static_cast<Context*>(ctx)->forced_dp = tiles;
+  return SYS1HIP_OK;
+}
+
 int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epilogue, char* name,
                          int64_t cap) {
   if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: null context");
@@ -306,11 +347,13 @@ int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epi
   const Context* c = static_cast<const Context*>(ctx);
   if (M <= 0 || N <= 0 || K <= 0)
     return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: bad shape");
-  int id, grid;
-  resolve(c, M, N, K, &id, &grid);
+  const Plan p = resolve(c, M, N, K);
+  const int id = p.kernel;
   if (name && cap > 0) {
     std::string s = kKernels[id].name;
-    s += "_g" + std::to_string(grid);
+    s += "_g" + std::to_string(p.grid);
+    const int64_t tiles = cdiv(M, kKernels[id].bm) * cdiv(N, kKernels[id].bn);
+    if (kKernels[id].streamk && p.dp > 0 && p.dp < tiles) s += "_dp" + std::to_string(p.dp);
     snprintf(name, (size_t)cap, "%s", s.c_str());
   }
   return id;
@@ -354,11 +397,11 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
 
   int rc = use_device(c);
   if (rc) return rc;
-  int id, grid;
-  resolve(c, M, N, K, &id, &grid);
-  const KernelEntry& e = kKernels[id];
-  if (e.streamk && cdiv(M, e.bm) * cdiv(N, e.bn) > kCounterSlots)
-    return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: more tiles than stream-K counters");
+  const Plan p = resolve(c, M, N, K);
+  const KernelEntry& e = kKernels[p.kernel];
+  const int64_t grid = p.grid;
+  if (e.streamk && cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp > kCounterSlots)
+    return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: more split tiles than stream-K counters");
 
   GemmArgs a;
   a.x = reinterpret_cast<const __bf16*>(x);
@@ -370,6 +413,7 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
   a.counters = c->counters;
   a.ldx = ldx, a.ldw = ldw, a.ldr = ldr, a.ldy = ldy;
   a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)nout;
+  a.dp_tiles = (int)std::min<int64_t>(p.dp, 1 << 30);
 
   if (grid <= 0 || grid > 0x7fffffff)
     return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: grid of %lld workgroups", (long long)grid);

@@ -45,6 +45,11 @@ class HipDevice:
         """Force the persistent grid size (0: automatic)."""
         _lib.check(self._L.sys1hip_set_grid(self.ctx, int(workgroups)), self.ctx)
 
+    def set_dp_tiles(self, tiles: int) -> None:
+        """Force the tiles a stream-K kernel runs whole before its stream
+        phase (-1 = automatic)."""
+        _lib.check(self._L.sys1hip_set_dp_tiles(self.ctx, int(tiles)), self.ctx)
+
     def query_kernel(self, M: int, N: int, K: int, epilogue: int = 0) -> tuple[int, str]:
         buf = ctypes.create_string_buffer(96)
         kid = _lib.check(self._L.sys1hip_query_kernel(self.ctx, M, N, K, epilogue, buf, 96), self.ctx)

@@ -134,4 +134,6 @@ def test_query_and_set_kernel_validate():
     assert L.sys1hip_set_kernel(None, 0) == _lib.EINVAL
     assert L.sys1hip_set_grid(None, 0) == _lib.EINVAL
     assert L.sys1hip_set_grid(_ctx, -1) == _lib.EINVAL
+    assert L.sys1hip_set_dp_tiles(None, 0) == _lib.EINVAL
+    assert L.sys1hip_set_dp_tiles(_ctx, -2) == _lib.EINVAL
     assert L.sys1hip_query_kernel(None, 1, 1, 8, 0, None, 0) == _lib.EINVAL

@@ -205,6 +205,69 @@ def test_stream_k_is_deterministic_and_rearms(dev, orc):
         dev.set_kernel(-1)
 
 
+@pytest.mark.parametrize("kname", ["stream_128x128_s2_w2x2", "stream_128x256_s2_w2x4"])
+def test_hybrid_tile_then_stream_phase(dev, orc, kname):
+    """Stream-K kernels on large M: the first dp tiles run whole, the rest
+    are split over every workgroup.  Every split (pure stream-K, one tile
+    whole, half, all but one, all) and small grids (several tiles per
+    workgroup in both phases) agree with the oracle, bit-identically across
+    repeats."""
+    from sys1_amd import kernel_names
+    from sys1_amd.linear import GatedLinear, Linear
+    M, N, K = 1000, 768, 328
+    bm, bn = (int(v) for v in kname.split("_")[1].split("x"))
+    tiles = -(-M // bm) * -(-N // bn)
+    x, w = _inputs(orc, M, N, K, 31)
+    xb, wb = orc.round_bf16(x), orc.round_bf16(w)
+    proj = orc.linear_f64(xb, wb).astype(np.float32)
+    p16 = orc.round_bf16(proj)
+    res = orc.fill_normal((M, N), 5)
+    ref_res = orc.round_bf16(p16 + orc.round_bf16(res))
+    I = N // 2
+    ref_geglu = orc.round_bf16(orc.round_bf16(orc.gelu_erf(p16[:, :I])) * p16[:, I:])
+    xg, wg, rg = to_gpu_bf16(x, torch), to_gpu_bf16(w, torch), to_gpu_bf16(res, torch)
+    lin, glu = Linear(wg, device=dev), GatedLinear(wg, "gelu", device=dev)
+    dev.set_kernel(kernel_names().index(kname))
+    try:
+        for g in (3, 7, 40):
+            dev.set_grid(g)
+            for dp in sorted({0, 1, tiles // 2, tiles - 1, tiles}):
+                dev.set_dp_tiles(dp)
+                print(f"[gpu] hybrid {kname} grid={g} dp={dp} tiles={tiles} "
+                      f"{dev.query_kernel(M, N, K)[1]}", flush=True)
+                y = to_np(lin(xg))
+                _check_close_to_rounded(orc, y, proj, f"{kname} g={g} dp={dp} none")
+                np.testing.assert_array_equal(y, to_np(lin(xg)))
+                y = to_np(lin(xg, residual=rg))
+                assert np.abs(y - ref_res).max() <= 2 * bf16_ulp(np.abs(ref_res).max())
+                y = to_np(glu(xg))
+                assert_parity(y, ref_geglu, f"{kname} g={g} dp={dp} geglu")
+    finally:
+        dev.set_dp_tiles(-1)
+        dev.set_grid(0)
+        dev.set_kernel(-1)
+
+
+def test_tile_kernel_small_forced_grid(dev, orc):
+    """A persistent tile grid smaller than the 8 XCDs still covers every tile."""
+    from sys1_amd import kernel_names
+    from sys1_amd.linear import Linear
+    M, N, K = 700, 640, 200
+    x, w = _inputs(orc, M, N, K, 41)
+    proj = orc.linear_f64(orc.round_bf16(x), orc.round_bf16(w)).astype(np.float32)
+    lin = Linear(to_gpu_bf16(w, torch), device=dev)
+    xg = to_gpu_bf16(x, torch)
+    dev.set_kernel(kernel_names().index("tile_128x128_s2_w2x2"))
+    try:
+        for g in (1, 3, 8, 9, 13):
+            dev.set_grid(g)
+            print(f"[gpu] tile grid={g} {dev.query_kernel(M, N, K)[1]}", flush=True)
+            _check_close_to_rounded(orc, to_np(lin(xg)), proj, f"tile grid={g}")
+    finally:
+        dev.set_grid(0)
+        dev.set_kernel(-1)
+
+
 def test_python_errors(dev, orc):
     from sys1_amd import Sys1HipError
     from sys1_amd.linear import GatedLinear, Linear
