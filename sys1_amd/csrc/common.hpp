@@ -105,7 +105,7 @@ struct GemmArgs {
   const __bf16* resid;  // [M, Nout] ld ldr or null
   __bf16* y;            // [M, Nout] ld ldy
   float* ws;            // stream-K partials (head/tail slot per workgroup)
-  unsigned* counters;   // stream-K arrival counter per tile (zero between calls)
+  unsigned* counters;   // stream-K arrival counter per (split tile, wave) (zero between calls)
   int64_t ldx, ldw, ldr, ldy;
   int M, N, K, Nout;
   int dp_tiles;         // stream-K kernels: tiles run whole before the stream phase

@@ -40,10 +40,11 @@
 //          phase of whole tiles: the hybrid schedule of TileWalk).  A range covers at
 //          most a partial head segment, whole tiles, and a partial tail
 //          segment; a partial segment writes its f32 accumulators to the
-//          workspace (head or tail slot of its workgroup), and the last
-//          segment of a tile to arrive (an arrival counter per tile) sums the
-//          tile's partials in workgroup order -- deterministic whatever the
-//          arrival order -- applies the epilogue and re-arms the counter.
+//          workspace (head or tail slot of its workgroup), and, per wave
+//          slice of the tile, the last owner to arrive (an arrival counter
+//          per tile and wave) sums the slice's partials in workgroup order --
+//          deterministic whatever the arrival order -- applies the epilogue
+//          to it and re-arms the counter.
 #pragma once
 
 #include "common.hpp"
@@ -240,8 +241,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
   using S = TileShape<BM, BN, WM, WN, STAGES, BK_>;
   constexpr int BK = S::BK;
   __shared__ __attribute__((aligned(1024))) char lds[S::kLdsBytes];
-  __shared__ int arrival_flag;  // stream-K: the tile's last owner
-  static_assert(!STREAMK || S::kLdsBytes + 16 <= 160 * 1024, "LDS budget with the arrival flag");
 
   const TileWalk walk(a.M, a.N, a.K, BM, BN, BK, STREAMK ? a.dp_tiles : 1 << 30);
   if (walk.steps() == 0) return;
@@ -474,20 +473,17 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
       }
     int g_lo, g_hi;
     walk.tile_owners(t, g_lo, g_hi);
-    __builtin_amdgcn_s_waitcnt(0);  // every wave: its partial stores are acknowledged
-    __syncthreads();
-    // The arrival result goes through an LDS word, with a second barrier
-    // before the next partial may overwrite it.
-    volatile int* flag = &arrival_flag;
-    if (tid == 0) {
-      const unsigned prev = __hip_atomic_fetch_add(a.counters + t, 1u, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-      *flag = prev == (unsigned)(g_hi - g_lo);
-    }
-    __syncthreads();
-    const bool last = *flag != 0;
-    __syncthreads();
-    if (!last) return false;
+    // Each wave arrives on its own counter (tile, wave): its slice of the
+    // tile (its accumulators, its epilogue) is independent of the other
+    // waves', so the last owner of each slice sums and stores that slice
+    // alone -- no barrier and no LDS.  Waves of one workgroup may disagree
+    // about being last; every slice still has exactly one last owner.
+    unsigned* counter = a.counters + (int64_t)t * S::kWaves + wave;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores are acknowledged
+    unsigned prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev != (unsigned)(g_hi - g_lo)) return false;
     zero_acc();
     const int64_t tile_lo = (int64_t)t * walk.kt_count;
     for (int g = g_lo; g <= g_hi; ++g) {
@@ -508,8 +504,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
           __builtin_amdgcn_sched_barrier(0);
         }
     }
-    if (tid == 0)
-      __hip_atomic_store(a.counters + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
   };
 

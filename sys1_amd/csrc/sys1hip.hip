@@ -19,7 +19,7 @@ namespace {
 
 constexpr int kVersion = 100;                        // 0.1.0
 constexpr size_t kWorkspaceBytes = 64ull << 20;      // stream-K partials
-constexpr int kCounterSlots = 1 << 16;               // stream-K arrival counters (tiles)
+constexpr int kCounterSlots = 1 << 16;               // stream-K arrival counters (tile x wave)
 
 thread_local std::string g_last_error;
 
@@ -62,12 +62,13 @@ struct KernelEntry {
   float efficiency;     // measured MFMA efficiency of the shape, fitted to a sweep of the
                         // projection shapes (ModernBERT base/large, Qwen, square)
   int bk;               // k-tile depth
+  int stages;           // LDS pipeline stages (stages - 1 k-tiles in flight)
   KernelFn fn[kEpiCount];
 };
 
 template <int BM, int BN, int WM, int WN, int ST, int BK, bool SK>
 constexpr KernelEntry tile_entry(const char* name, int occ, float eff) {
-  return KernelEntry{name, BM, BN, WM * WN * 64, occ, SK, eff, BK,
+  return KernelEntry{name, BM, BN, WM * WN * 64, occ, SK, eff, BK, ST,
                      {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 0>, gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 1>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 2>, gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 3>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 4>, gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 5>,
@@ -78,14 +79,16 @@ constexpr KernelEntry tile_entry(const char* name, int occ, float eff) {
 // "stream" group serves small M (weight-streaming: BM = padded token count,
 // BN = 256, deep stages, K split over workgroups).
 const KernelEntry kKernels[] = {
-    tile_entry<256, 256, 2, 4, 2, 64, false>("tile_256x256_s2_w2x4", 1, 1.00f),
+    tile_entry<256, 256, 2, 4, 2, 64, false>("tile_256x256_s2_w2x4", 1, 0.80f),
     tile_entry<128, 256, 2, 4, 2, 64, false>("tile_128x256_s2_w2x4", 1, 0.40f),
     tile_entry<128, 192, 4, 2, 2, 64, false>("tile_128x192_s2_w4x2", 1, 0.40f),
-    tile_entry<128, 128, 2, 2, 2, 64, false>("tile_128x128_s2_w2x2", 2, 0.80f),
+    tile_entry<128, 128, 2, 2, 2, 64, false>("tile_128x128_s2_w2x2", 2, 0.60f),
     tile_entry<32, 256, 1, 4, 4, 64, true>("stream_32x256_s4_w1x4", 1, 0.50f),
     tile_entry<64, 256, 2, 4, 3, 64, true>("stream_64x256_s3_w2x4", 1, 0.60f),
-    tile_entry<128, 128, 2, 2, 2, 64, true>("stream_128x128_s2_w2x2", 2, 0.80f),
-    tile_entry<128, 256, 2, 4, 2, 64, true>("stream_128x256_s2_w2x4", 1, 0.80f),
+    tile_entry<64, 256, 2, 4, 4, 64, true>("stream_64x256_s4_w2x4", 1, 0.60f),
+    tile_entry<128, 128, 2, 2, 4, 64, true>("stream_128x128_s4_w2x2", 1, 0.80f),
+    tile_entry<128, 256, 2, 4, 3, 64, true>("stream_128x256_s3_w2x4", 1, 0.80f),
+    tile_entry<256, 128, 4, 2, 3, 64, true>("stream_256x128_s3_w4x2", 1, 0.80f),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
@@ -107,17 +110,22 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Modelled time (in CU clocks) of a projection on kernel `e` launched on
 // `grid` workgroups, of which the first `dp` tiles run whole (tile phase)
 // and the rest are split over every workgroup (stream phase; stream-K
-// kernels only).  A tile's cycles per k-tile are the larger of its MFMA
-// cycles (derated by the shape's measured efficiency) and its operand loads
-// at about 48 B/clk per CU from L2; workgroups sharing a CU share its time.
+// kernels only).  A k-tile costs a workgroup the larger of
+//   - its compute: MFMA cycles (derated by the shape's fitted efficiency) or
+//     operand loads at kLoadBytesPerClk per CU, times the workgroups sharing
+//     the CU, and
+//   - the load latency spread over the k-tiles in flight (stages - 1).
 // A split tile costs its last arriving owner the arrival latency plus
-// reading every owner's f32 partial.  The whole call is bounded below by the
-// chip's HBM time for the weights.
+// reading every owner's f32 partial.  The call is bounded below by the
+// weight bytes at a sustained HBM rate.  The constants and efficiencies are
+// fitted to measured projection shapes (ModernBERT base/large in their
+// chains, Qwen 27B at M = 128, square large GEMMs).
 constexpr double kFlopPerClk = 4096.0;      // bf16 MFMA per CU per clock
-constexpr double kLoadBytesPerClk = 48.0;   // L2 -> CU
+constexpr double kLoadBytesPerClk = 48.0;   // L2 -> LDS per CU
 constexpr double kStoreBytesPerClk = 64.0;
-constexpr double kHbmBytesPerClk = 3000.0;  // ~6.6 TB/s sustained at ~2.2 GHz, whole chip
-constexpr double kFixupClk = 6000.0;        // partial write + arrival latency
+constexpr double kHbmBytesPerClk = 1500.0;  // whole chip, sustained by a weight stream
+constexpr double kFixupClk = 2000.0;        // partial write + arrival
+constexpr double kLatencyClk = 1500.0;      // load issue -> data in LDS
 
 struct Plan {
   int kernel = 0;
@@ -130,19 +138,18 @@ double model_cost(const Context* c, const KernelEntry& e, int64_t M, int64_t N, 
                   int64_t grid, int64_t dp) {
   const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
   const int64_t kts = cdiv(K, e.bk);
-  const double mfma = 2.0 * e.bm * e.bn * e.bk / kFlopPerClk / e.efficiency;  // per k-tile
-  const double load = (double)(e.bm + e.bn) * e.bk * 2.0 / kLoadBytesPerClk;
-  const double per_kt = std::max(mfma, load);
-  const double store = 2.0 * e.bm * e.bn / kStoreBytesPerClk;
-  const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk;
   const double share = std::max(1.0, (double)grid / c->cus);  // workgroups per CU
-  double t = (double)cdiv(dp, grid) * share * (kts * per_kt + store);
+  const double mfma = 2.0 * e.bm * e.bn * e.bk / kFlopPerClk / e.efficiency;
+  const double load = (double)(e.bm + e.bn) * e.bk * 2.0 / kLoadBytesPerClk;
+  const double per_kt = std::max(share * std::max(mfma, load), kLatencyClk / (e.stages - 1));
+  const double store = share * 2.0 * e.bm * e.bn / kStoreBytesPerClk;
+  const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk;
+  double t = (double)cdiv(dp, grid) * (kts * per_kt + store);
   const int64_t st = tiles - dp;
   if (st > 0) {
     const int64_t total = st * kts;
     const int64_t sg = std::min(grid, total);  // workgroups in the stream phase
-    const double iters = (double)cdiv(total, sg);
-    t += share * (iters * per_kt + ((double)cdiv(st, sg) + 1.0) * store);
+    t += (double)cdiv(total, sg) * per_kt + ((double)cdiv(st, sg) + 1.0) * store;
     if (total % sg != 0 || sg > st) {
       const double owners = std::min<double>((double)sg, (double)sg / st + 1.0);
       t += kFixupClk + owners * e.bm * e.bn * 4.0 / kLoadBytesPerClk;
@@ -180,7 +187,7 @@ void consider(const Context* c, int id, int64_t M, int64_t N, int64_t K, int64_t
     if (whole == tiles) cand[1] = tiles;
   }
   for (int64_t dp : cand) {
-    if (dp < 0 || tiles - dp > kCounterSlots) continue;
+    if (dp < 0 || (tiles - dp) * (e.threads / 64) > kCounterSlots) continue;
     const double cost = model_cost(c, e, M, N, K, grid, dp);
     if (cost < best->cost * 0.999) {
       best->kernel = id, best->grid = grid, best->dp = dp, best->cost = cost;
@@ -400,7 +407,7 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
   const Plan p = resolve(c, M, N, K);
   const KernelEntry& e = kKernels[p.kernel];
   const int64_t grid = p.grid;
-  if (e.streamk && cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp > kCounterSlots)
+  if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
     return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: more split tiles than stream-K counters");
 
   GemmArgs a;
