@@ -236,8 +236,9 @@ struct TileWalk {
 
 // STREAMK: stream-K schedule (the weight-streaming shapes); the large-M
 // shapes compile the tile schedule only.
-template <int BM, int BN, int WM, int WN, int STAGES, int BK_, bool STREAMK, int EPI>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
+// OCC: resident workgroups per CU the register allocation must allow.
+template <int BM, int BN, int WM, int WN, int STAGES, int BK_, int OCC, bool STREAMK, int EPI>
+__global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a) {
   using S = TileShape<BM, BN, WM, WN, STAGES, BK_>;
   constexpr int BK = S::BK;
   __shared__ __attribute__((aligned(1024))) char lds[S::kLdsBytes];
@@ -526,23 +527,50 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
 
   Segment csg = walk.first_segment();  // compute cursor
   int ckt = csg.kt0;
-  Frags fr[2];  // ping-pong fragment sets: k-step ks reads into fr[ks % 2]
-  if (steps > 0) read(fr[0], 0, 0);
+  // Two schedules of a k-tile's KS k-steps of MFMAs (fragment reads one
+  // k-step ahead of their MFMAs in both):
+  //   kDeep (one fragment set per k-step, when they fit in registers): the
+  //     barrier that frees the stage comes after the k-tile's last two
+  //     fragment sets are in registers, so two k-steps of MFMAs run after it,
+  //     covering the next stage's first fragment reads, with the freed
+  //     stage's refill issued between them;
+  //   otherwise (ping-pong sets): one k-step of MFMAs after the barrier.
+  constexpr int kReads = S::FM + S::FN;  // LDS reads per fragment set
+  constexpr bool kDeep = S::KS == 4 && kReads * 4 * 4 <= 64;
+  constexpr int kSets = kDeep ? 4 : 2;
+  Frags fr[kSets];
+  if (steps > 0) {
+    read(fr[0], 0, 0);
+    if constexpr (kDeep) read(fr[1], 0, 1);
+  }
   int stage = 0;
   for (int s = 0; s < steps; ++s) {
-    // The k-tile's first fragments (read before the previous k-tile's last
-    // MFMAs) are in.  Waiting for them here, explicitly, keeps the compiler
-    // from resolving its merged loop-header state with a full LDS wait placed
-    // after the next fragment reads, which would serialise LDS latency with
-    // every k-tile's first MFMAs.
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt unconstrained
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kDeep) {
+      // fr[0] (and fr[1], one set later) of this k-tile were read after the
+      // previous barrier.  Waiting for them explicitly keeps the compiler
+      // from resolving its merged loop-header state with a full LDS wait
+      // after the next reads.
+      __builtin_amdgcn_s_waitcnt(0xc07f | (kReads << 8));  // lgkmcnt(kReads): fr[0] is in
+      __builtin_amdgcn_sched_barrier(0);
+      read(fr[2], stage, 2);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(fr[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      read(fr[3], stage, 3);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(fr[1]);
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      // As above: the k-tile's first fragments are in.
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt unconstrained
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int ks = 1; ks < S::KS; ++ks) {
-      read(fr[ks % 2], stage, ks);
-      __builtin_amdgcn_sched_barrier(0);
-      mma(fr[(ks - 1) % 2]);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int ks = 1; ks < S::KS; ++ks) {
+        read(fr[ks % 2], stage, ks);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fr[(ks - 1) % 2]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     if (s + 1 < steps) {
       if (s + STAGES - 1 < steps) vm_wait<(STAGES - 2) * S::kDma>();
@@ -555,12 +583,25 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_tile_kernel(GemmArgs a) {
     // that stall overlaps matrix work instead of delaying it.
     const int freed = stage;
     stage = stage + 1 == STAGES ? 0 : stage + 1;
-    if (s + 1 < steps) read(fr[0], stage, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(fr[(S::KS - 1) % 2]);
-    __builtin_amdgcn_sched_barrier(0);
-    if (s + STAGES < steps) issue(freed);
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (kDeep) {
+      if (s + 1 < steps) read(fr[0], stage, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(fr[2]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + STAGES < steps) issue(freed);
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 1 < steps) read(fr[1], stage, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(fr[3]);
+      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      if (s + 1 < steps) read(fr[0], stage, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(fr[(S::KS - 1) % 2]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + STAGES < steps) issue(freed);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if (++ckt == csg.kt1) {
       if constexpr (STREAMK) {
         if (walk.complete(csg) || finish_partial(csg)) epilogue(csg.tm * BM, csg.tn * BN);

@@ -66,29 +66,32 @@ struct KernelEntry {
   KernelFn fn[kEpiCount];
 };
 
-template <int BM, int BN, int WM, int WN, int ST, int BK, bool SK>
-constexpr KernelEntry tile_entry(const char* name, int occ, float eff) {
-  return KernelEntry{name, BM, BN, WM * WN * 64, occ, SK, eff, BK, ST,
-                     {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 0>, gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 1>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 2>, gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 3>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 4>, gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 5>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, SK, 6>}};
+template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK>
+constexpr KernelEntry tile_entry(const char* name, float eff) {
+  return KernelEntry{name, BM, BN, WM * WN * 64, OCC, SK, eff, BK, ST,
+                     {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 0>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 1>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 2>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 3>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 4>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 5>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 6>}};
 }
 
 // Output-tile shapes.  The first group serves large M (MFMA-bound); the
 // "stream" group serves small M (weight-streaming: BM = padded token count,
 // BN = 256, deep stages, K split over workgroups).
 const KernelEntry kKernels[] = {
-    tile_entry<256, 256, 2, 4, 2, 64, false>("tile_256x256_s2_w2x4", 1, 0.80f),
-    tile_entry<128, 256, 2, 4, 2, 64, false>("tile_128x256_s2_w2x4", 1, 0.40f),
-    tile_entry<128, 192, 4, 2, 2, 64, false>("tile_128x192_s2_w4x2", 1, 0.40f),
-    tile_entry<128, 128, 2, 2, 2, 64, false>("tile_128x128_s2_w2x2", 2, 0.60f),
-    tile_entry<32, 256, 1, 4, 4, 64, true>("stream_32x256_s4_w1x4", 1, 0.50f),
-    tile_entry<64, 256, 2, 4, 3, 64, true>("stream_64x256_s3_w2x4", 1, 0.60f),
-    tile_entry<64, 256, 2, 4, 4, 64, true>("stream_64x256_s4_w2x4", 1, 0.60f),
-    tile_entry<128, 128, 2, 2, 4, 64, true>("stream_128x128_s4_w2x2", 1, 0.80f),
-    tile_entry<128, 256, 2, 4, 3, 64, true>("stream_128x256_s3_w2x4", 1, 0.80f),
-    tile_entry<256, 128, 4, 2, 3, 64, true>("stream_256x128_s3_w4x2", 1, 0.80f),
+    tile_entry<256, 256, 2, 4, 2, 64, 1, false>("tile_256x256_s2_w2x4", 0.80f),
+    tile_entry<128, 256, 2, 4, 2, 64, 1, false>("tile_128x256_s2_w2x4", 0.40f),
+    tile_entry<128, 192, 4, 2, 2, 64, 1, false>("tile_128x192_s2_w4x2", 0.40f),
+    tile_entry<128, 128, 2, 2, 2, 64, 2, false>("tile_128x128_s2_w2x2", 0.60f),
+    tile_entry<32, 256, 1, 4, 4, 64, 1, true>("stream_32x256_s4_w1x4", 0.50f),
+    tile_entry<64, 256, 2, 4, 3, 64, 1, true>("stream_64x256_s3_w2x4", 0.60f),
+    tile_entry<64, 256, 2, 4, 4, 64, 1, true>("stream_64x256_s4_w2x4", 0.60f),
+    tile_entry<128, 128, 2, 2, 4, 64, 1, true>("stream_128x128_s4_w2x2", 0.80f),
+    tile_entry<128, 256, 2, 4, 3, 64, 1, true>("stream_128x256_s3_w2x4", 0.80f),
+    tile_entry<256, 128, 4, 2, 3, 64, 1, true>("stream_256x128_s3_w4x2", 0.80f),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
@@ -196,8 +199,9 @@ void consider(const Context* c, int id, int64_t M, int64_t N, int64_t K, int64_t
 }
 
 // Plan of a call: the cheapest modelled (kernel, grid, dp) over the shapes
-// allowed for M (stream-K shapes where M fits their tile height, tile shapes
-// above 128 tokens), or over the forced kernel, grid and/or dp.  Stream-K grids from a quarter of
+// allowed for M (stream-K shapes where M fits their tile height or their
+// tiles cannot fill the CUs, tile shapes above 128 tokens), or over the
+// forced kernel, grid and/or dp.  Stream-K grids from a quarter of
 // the slots up to all of them are tried.
 Plan resolve(const Context* c, int64_t M, int64_t N, int64_t K) {
   Plan best;
@@ -207,8 +211,9 @@ Plan resolve(const Context* c, int64_t M, int64_t N, int64_t K) {
     if (c->forced_kernel < 0) {
       // Measured in the projection chains: the large-M hybrid loses to the
       // plain tile schedule (every split tile moves two f32 partials across
-      // the fabric), so stream-K is chosen only where M fits one tile row.
-      if (e.streamk && M > e.bm) continue;
+      // the fabric), so stream-K is offered where M fits one tile row, or
+      // where the tiles cannot fill the CUs (few tiles, deep K).
+      if (e.streamk && M > e.bm && cdiv(M, e.bm) * cdiv(N, e.bn) >= c->cus) continue;
       if (!e.streamk && M <= 128) continue;
     }
     const int64_t gmax = max_grid(c, e, M, N, K);
