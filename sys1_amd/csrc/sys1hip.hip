@@ -211,9 +211,11 @@ Plan resolve(const Context* c, int64_t M, int64_t N, int64_t K) {
     if (c->forced_kernel < 0) {
       // Measured in the projection chains: the large-M hybrid loses to the
       // plain tile schedule (every split tile moves two f32 partials across
-      // the fabric), so stream-K is offered where M fits one tile row, or
-      // where the tiles cannot fill the CUs (few tiles, deep K).
-      if (e.streamk && M > e.bm && cdiv(M, e.bm) * cdiv(N, e.bn) >= c->cus) continue;
+      // the fabric), so stream-K is offered where M fits one tile row, or,
+      // above 256 tokens, where the tiles cannot fill the CUs (few tiles,
+      // deep K).  Up to 256 tokens the weight stream dominates, and a tile
+      // shorter than M would stream the weight once per tile row.
+      if (e.streamk && M > e.bm && (M <= 256 || cdiv(M, e.bm) * cdiv(N, e.bn) >= c->cus)) continue;
       if (!e.streamk && M <= 128) continue;
     }
     const int64_t gmax = max_grid(c, e, M, N, K);
