@@ -256,12 +256,14 @@ def test_projection_stack_matches_module_chain(dev, orc):
     assert torch.equal(out, h)
 
 
-@pytest.mark.parametrize("M", [64, 1024])
-def test_modernbert_large_chain(dev, orc, M):
-    """BASELINE config 3 shapes (hidden 1024, GeGLU 2x2624), first 4 layers,
-    skinny (M=64) and tiled (M=1024) regimes."""
+@pytest.mark.parametrize("M,layers", [(64, 4), (256, 4), (1024, 4), (4096, 2), (16384, 1)])
+def test_modernbert_large_chain(dev, orc, M, layers):
+    """BASELINE config 3 shapes (hidden 1024, GeGLU 2x2624) over its whole M
+    sweep {64, 256, 1024, 4096, 16384}: weight-streaming stream-K (64, 256),
+    128x128 tiles with deep-K stream-K (1024), 128x128 and 256x256 tiles
+    (4096, 16384).  Fewer layers at large M keep the CPU oracle to seconds."""
     from sys1_amd.stacks import modernbert
-    cfg = modernbert(1024, 2624, 4, "modernbert-large-4")
+    cfg = modernbert(1024, 2624, layers, f"modernbert-large-{layers}")
     print(f"[gpu] modernbert-large 4 layers M={M}", flush=True)
     x = orc.fill_normal((M, 1024), 21)
     ws = _weights(orc, cfg, 500)
@@ -271,14 +273,17 @@ def test_modernbert_large_chain(dev, orc, M):
     assert rel < CHAIN_TOL
 
 
-@pytest.mark.parametrize("name,M", [("qwen35-small", 256), ("qwen35-small", 1000),
-                                    ("qwen35-27b", 128)])
-def test_qwen_layers(dev, orc, name, M):
-    """One DeltaNet layer and one gated-attention layer of the Qwen3.5-style
-    configs (4 and 5), at their real projection shapes, per projection."""
+@pytest.mark.parametrize("name,M,both", [("qwen35-small", 256, True), ("qwen35-small", 1000, True),
+                                         ("qwen35-small", 8192, False), ("qwen35-27b", 128, True),
+                                         ("qwen35-27b", 1024, False)])
+def test_qwen_layers(dev, orc, name, M, both):
+    """One DeltaNet layer and (where `both`) one gated-attention layer of the
+    Qwen3.5-style configs (4 and 5), at their real projection shapes and the
+    BASELINE token counts (config 4: exactly 8192; config 5: 128 and 1024),
+    per projection."""
     from sys1_amd.stacks import CONFIGS, StackConfig
     full = CONFIGS[name]()
-    cfg = StackConfig(name, full.hidden, [full.layers[0], full.layers[3]])
+    cfg = StackConfig(name, full.hidden, [full.layers[0], full.layers[3]] if both else [full.layers[0]])
     print(f"[gpu] {name} DeltaNet + attention layer M={M}", flush=True)
     x = orc.fill_normal((M, full.hidden), 31)
     ws = _weights(orc, cfg, 700)
