@@ -126,6 +126,29 @@ SYS1HIP_API int sys1hip_set_kernel(void* ctx, int32_t kernel_id);
  * ranges, clamped to the iteration count and to what the workspace holds. */
 SYS1HIP_API int sys1hip_set_grid(void* ctx, int32_t workgroups);
 
+/* Wqkv with the rotary embedding fused into the epilogue: replaces the
+ * projection at src/archs/modernbert.rs:184-187 followed by the fused
+ * RoPE + q/k/v split of src/archs/modernbert.rs:112-120 /
+ * src/kernels/modernbert.cu:31-74 (rope_qkv).
+ *   x [M, K] (packed tokens), w [3H, K] with q | k | v row blocks,
+ *   H = heads * head_dim, head_dim = 64 (ModernBERT base and large);
+ *   rope_cos, rope_sin: f32 [rope_rows, head_dim/2] device tables
+ *   (RotaryEmbedding::new, src/archs/modernbert.rs:67-83), 16-byte aligned;
+ *   positions: int32 [M], token m's rotary position within its sequence
+ *   (the reference's padded rectangle uses token % length), each in
+ *   [0, rope_rows); the kernel clamps values outside that range into it, so
+ *   a bad position never reads outside the tables;
+ *   qkv: bf16 [3][M][H] output planes q, k, v, each [M, heads, head_dim] --
+ *   the packed (varlen) attention layout.
+ * Per element: the projection is rounded to bf16, rotated in f32
+ * (x0 cos - x1 sin, x0 sin + x1 cos over columns c, c + 32 of a head) and
+ * rounded once; v is the rounded projection. */
+SYS1HIP_API int sys1hip_linear_rope_qkv_bf16(void* ctx, const uint16_t* x, int64_t ldx,
+                                             const uint16_t* w, int64_t ldw, const float* rope_cos,
+                                             const float* rope_sin, int64_t rope_rows,
+                                             const int32_t* positions, uint16_t* qkv, int64_t M,
+                                             int64_t heads, int64_t head_dim, int64_t K);
+
 /* Tuning and test knob, no counterpart in the reference: force how many
  * tiles a stream-K kernel runs whole before its stream phase, for every
  * later call on this context (-1 = automatic; clamped to the tile count).

@@ -258,3 +258,54 @@ ORC_EXPORT void orc_silu_array(const float* in, float* out, int64_t n) {
     #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) out[i] = orc_silu(in[i]);
 }
+
+/* ---------------------------------------------------------------- RoPE ---- */
+
+/* Rotary tables of ModernBERT's RotaryEmbedding::new
+ * (src/archs/modernbert.rs:67-83): dim = hidden / heads, inv_freq[i] =
+ * 1 / theta^(2i / dim) for i < dim/2 (the f64 power rounded to f32),
+ * frequencies = positions (f32) x inv_freq (an f32 outer product),
+ * cos/sin [positions, dim/2] in f32. */
+ORC_EXPORT void orc_rope_tables(double theta, int64_t dim, int64_t positions, float* cos_out,
+                                float* sin_out) {
+  const int64_t half = dim / 2;
+  for (int64_t p = 0; p < positions; ++p)
+    for (int64_t i = 0; i < half; ++i) {
+      const float inv = 1.0f / (float)pow(theta, (double)(2 * i) / (double)dim);
+      const float f = (float)p * inv;
+      cos_out[p * half + i] = cosf(f);
+      sin_out[p * half + i] = sinf(f);
+    }
+}
+
+/* Fused RoPE + q/k/v split of src/kernels/modernbert.cu:31-74 (rope_qkv),
+ * as the Wqkv epilogue sees it on packed tokens.  qkv [M, 3*heads*dim]
+ * holds q | k | v blocks; for token m (rotary position pos[m]), head h and
+ * column c < dim/2, with x0 = q[c], x1 = q[c + dim/2]:
+ *   out_q[c]          = x0 * cos - x1 * sin
+ *   out_q[c + dim/2]  = x0 * sin + x1 * cos
+ * the same for k, and v copied.  Output planes out[3][M][heads*dim].  The
+ * reference indexes positions as token % length on its padded rectangle;
+ * packed tokens carry their position within their sequence instead. */
+ORC_EXPORT void orc_rope_qkv(const float* qkv, int64_t ldqkv, const float* cos_t,
+                             const float* sin_t, const int32_t* pos, int64_t M, int64_t heads,
+                             int64_t dim, float* out) {
+  const int64_t half = dim / 2, H = heads * dim;
+  for (int64_t m = 0; m < M; ++m) {
+    const float* row = qkv + m * ldqkv;
+    const float* c = cos_t + (int64_t)pos[m] * half;
+    const float* s = sin_t + (int64_t)pos[m] * half;
+    for (int64_t h = 0; h < heads; ++h)
+      for (int64_t j = 0; j < half; ++j) {
+        for (int plane = 0; plane < 2; ++plane) {
+          const float x0 = row[plane * H + h * dim + j], x1 = row[plane * H + h * dim + j + half];
+          float* o = out + plane * M * H + m * H + h * dim;
+          o[j] = x0 * c[j] - x1 * s[j];
+          o[j + half] = x0 * s[j] + x1 * c[j];
+        }
+        float* ov = out + 2 * M * H + m * H + h * dim;
+        ov[j] = row[2 * H + h * dim + j];
+        ov[j + half] = row[2 * H + h * dim + j + half];
+      }
+  }
+}

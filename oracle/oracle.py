@@ -57,6 +57,9 @@ def lib():
         L.orc_pack_ragged.restype = _i64
         L.orc_gelu_erf_array.argtypes = [_f32p, _f32p, _i64]
         L.orc_silu_array.argtypes = [_f32p, _f32p, _i64]
+        L.orc_rope_tables.argtypes = [ctypes.c_double, _i64, _i64, _f32p, _f32p]
+        L.orc_rope_qkv.argtypes = [_f32p, _i64, _f32p, _f32p, ctypes.POINTER(ctypes.c_int32),
+                                   _i64, _i64, _i64, _f32p]
         _lib = L
     return _lib
 
@@ -219,3 +222,26 @@ def laya_scorer_f32(hidden_rows, ln_w, ln_b, w_in, b_in, w_out, b_out):
     z = layer_norm(hidden_rows, ln_w, ln_b, 1e-5)
     z = gelu_erf(linear_f32(z, w_in, b_in))
     return linear_f32(z, w_out, b_out)[:, 0]
+
+
+def rope_tables(theta: float, dim: int, positions: int):
+    """cos, sin [positions, dim/2] f32 of src/archs/modernbert.rs:67-83."""
+    half = dim // 2
+    c = np.empty((positions, half), np.float32)
+    s = np.empty((positions, half), np.float32)
+    lib().orc_rope_tables(float(theta), dim, positions, _p(c), _p(s))
+    return c, s
+
+
+def rope_qkv(qkv, cos, sin, positions, heads: int, dim: int) -> np.ndarray:
+    """Fused RoPE + q/k/v split (src/kernels/modernbert.cu:31-74) on packed
+    tokens: qkv [M, 3*heads*dim] -> planes [3, M, heads*dim]; positions[m] is
+    token m's rotary position within its sequence."""
+    qkv = _f32(qkv)
+    M = qkv.shape[0]
+    pos = np.ascontiguousarray(positions, np.int32)
+    assert pos.shape == (M,) and qkv.shape[1] == 3 * heads * dim
+    out = np.empty((3, M, heads * dim), np.float32)
+    lib().orc_rope_qkv(_p(qkv), qkv.shape[1], _p(_f32(cos)), _p(_f32(sin)),
+                       pos.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), M, heads, dim, _p(out))
+    return out

@@ -52,6 +52,17 @@ def cu_seqlens(lengths) -> np.ndarray:
     return np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
 
 
+def positions(lengths) -> np.ndarray:
+    """Per packed token, its position within its sequence (int32): the
+    rotary position the reference reads as token % length on its padded
+    rectangle (src/kernels/modernbert.cu:31-74)."""
+    lengths = np.asarray(lengths, dtype=np.int64)
+    if (lengths < 0).any():
+        raise ValueError("negative sequence length")
+    starts = np.repeat(cu_seqlens(lengths)[:-1], lengths)
+    return (np.arange(int(lengths.sum()), dtype=np.int64) - starts).astype(np.int32)
+
+
 def pack_rows(padded: np.ndarray, lengths) -> np.ndarray:
     """[batch, max_len, H] padded rectangle -> [sum(lengths), H] packed rows."""
     return np.concatenate([padded[b, :l] for b, l in enumerate(lengths)], 0)

@@ -26,7 +26,8 @@ enum Epi : int {
   kEpiResidual = 4,
   kEpiBiasGelu = 5,
   kEpiBiasResidual = 6,
-  kEpiCount = 7,
+  kEpiRopeQkv = 7,   // Wqkv: RoPE on q and k, q/k/v written as three planes
+  kEpiCount = 8,
 };
 
 __host__ __device__ constexpr bool epi_gated(int e) { return e == kEpiGeglu || e == kEpiSwiglu; }
@@ -109,6 +110,14 @@ struct GemmArgs {
   int64_t ldx, ldw, ldr, ldy;
   int M, N, K, Nout;
   int dp_tiles;         // stream-K kernels: tiles run whole before the stream phase
+  // kEpiRopeQkv: y holds planes q, k, v of [M, H] (H = Nout / 3, ld ldy),
+  // `plane` elements apart; head_dim 64; cos/sin [positions, 32] f32;
+  // pos[m] is token m's rotary position.
+  const float* rope_cos;
+  const float* rope_sin;
+  const int* pos;
+  int rope_rows;        // table rows: positions are clamped into [0, rope_rows)
+  int64_t plane;
 };
 
 // Map the hardware workgroup id to a logical tile id so that each XCD gets a

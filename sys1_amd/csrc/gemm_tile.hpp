@@ -387,7 +387,58 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
       const bool row_ok = m < a.M;
 #pragma unroll
       for (int i = 0; i < S::FN; ++i) {
-        if constexpr (epi_gated(EPI)) {
+        if constexpr (EPI == kEpiRopeQkv) {
+          // Blocks i (even) and i+1 are the two halves of one 64-wide head
+          // (the plan guarantees 64-wide, head-aligned wave columns), so a
+          // lane holds columns c and c+32 of the same token: the rotation
+          // of src/kernels/modernbert.cu:31-74 happens in registers on the
+          // bf16-rounded projection, rounded once, and q, k and v go to
+          // their planes.
+          if (i % 2 == 0) {
+            const int nw = out_n0 + i * 32;  // head start column in qkv
+            const int H = a.Nout / 3;
+            const int p = nw / H;
+            const int col = nw - p * H;
+            const int pos = row_ok ? min(max(a.pos[m], 0), a.rope_rows - 1) : 0;  // stay inside the tables
+            bf16x4 lo[4], hi[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              float x0[4], x1[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                x0[e] = round_bf16(acc[i][j][4 * g + e]);
+                x1[e] = round_bf16(acc[i + 1][j][4 * g + e]);
+              }
+              if (p < 2) {
+                const int c = 8 * g + 4 * h;  // column within the half head
+                const f32x4 cs = *reinterpret_cast<const f32x4*>(a.rope_cos + (int64_t)pos * 32 + c);
+                const f32x4 sn = *reinterpret_cast<const f32x4*>(a.rope_sin + (int64_t)pos * 32 + c);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const float r0 = x0[e] * cs[e] - x1[e] * sn[e];
+                  const float r1 = x0[e] * sn[e] + x1[e] * cs[e];
+                  x0[e] = r0;
+                  x1[e] = r1;
+                }
+              }
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                lo[g][e] = to_bf16(x0[e]);
+                hi[g][e] = to_bf16(x1[e]);
+              }
+            }
+            __bf16* dst = a.y + p * a.plane + (int64_t)m * a.ldy + col;
+#pragma unroll
+            for (int gp = 0; gp < 2; ++gp) {
+              const bf16x8 vlo = pair16(lo[2 * gp], lo[2 * gp + 1]);
+              const bf16x8 vhi = pair16(hi[2 * gp], hi[2 * gp + 1]);
+              if (row_ok) {
+                store8(dst + 16 * gp + 8 * h, vlo, 8);
+                store8(dst + 32 + 16 * gp + 8 * h, vhi, 8);
+              }
+            }
+          }
+        } else if constexpr (epi_gated(EPI)) {
           // A 32-row block of the packed weight is 16 gate rows then the 16
           // up rows of the same 16 output columns: registers 4g+e (g = 0, 1)
           // hold gate rows, 4(g+2)+e the matching up rows.

@@ -63,19 +63,21 @@ struct KernelEntry {
                         // projection shapes (ModernBERT base/large, Qwen, square)
   int bk;               // k-tile depth
   int stages;           // LDS pipeline stages (stages - 1 k-tiles in flight)
+  int tn;               // output columns per wave (the RoPE epilogue needs 64: one head)
   KernelFn fn[kEpiCount];
 };
 
 template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK>
 constexpr KernelEntry tile_entry(const char* name, float eff) {
-  return KernelEntry{name, BM, BN, WM * WN * 64, OCC, SK, eff, BK, ST,
+  return KernelEntry{name, BM, BN, WM * WN * 64, OCC, SK, eff, BK, ST, BN / WN,
                      {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 0>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 1>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 2>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 3>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 4>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 5>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 6>}};
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 6>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 7>}};
 }
 
 // Output-tile shapes.  The first group serves large M (MFMA-bound); the
@@ -203,11 +205,12 @@ void consider(const Context* c, int id, int64_t M, int64_t N, int64_t K, int64_t
 // tiles cannot fill the CUs, tile shapes above 128 tokens), or over the
 // forced kernel, grid and/or dp.  Stream-K grids from a quarter of
 // the slots up to all of them are tried.
-Plan resolve(const Context* c, int64_t M, int64_t N, int64_t K) {
+Plan resolve(const Context* c, int64_t M, int64_t N, int64_t K, bool head64 = false) {
   Plan best;
   for (int id = 0; id < kNumKernels; ++id) {
     if (c->forced_kernel >= 0 && id != c->forced_kernel) continue;
     const KernelEntry& e = kKernels[id];
+    if (head64 && e.tn != 64) continue;
     if (c->forced_kernel < 0) {
       // Measured in the projection chains: the large-M hybrid loses to the
       // plain tile schedule (every split tile moves two f32 partials across
@@ -432,6 +435,59 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
   if (grid <= 0 || grid > 0x7fffffff)
     return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: grid of %lld workgroups", (long long)grid);
   hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)grid), dim3(e.threads), 0, c->stream, a);
+  HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+
+int sys1hip_linear_rope_qkv_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_t* w,
+                                 int64_t ldw, const float* rope_cos, const float* rope_sin,
+                                 int64_t rope_rows, const int32_t* positions, uint16_t* qkv,
+                                 int64_t M, int64_t heads, int64_t head_dim, int64_t K) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_linear_rope_qkv_bf16: null context");
+  Context* c = static_cast<Context*>(ctx);
+  if (M < 0 || heads <= 0 || K <= 0 || rope_rows <= 0 || rope_rows > (1ll << 30))
+    return fail(SYS1HIP_EINVAL,
+                "sys1hip_linear_rope_qkv_bf16: bad shape M=%lld heads=%lld K=%lld rope_rows=%lld",
+                (long long)M, (long long)heads, (long long)K, (long long)rope_rows);
+  if (head_dim != 64)
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_rope_qkv_bf16: head_dim %lld unsupported (64 only)",
+                (long long)head_dim);
+  if (M == 0) return SYS1HIP_OK;
+  if (!x || !w || !qkv || !rope_cos || !rope_sin || !positions)
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_rope_qkv_bf16: null pointer");
+  if (ldx < K || ldw < K)
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_rope_qkv_bf16: leading dimension below K");
+  if (K % 8 || ldx % 8 || ldw % 8)
+    return fail(SYS1HIP_EALIGN, "sys1hip_linear_rope_qkv_bf16: K, ldx and ldw must be multiples of 8");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(rope_cos) || !aligned16(rope_sin))
+    return fail(SYS1HIP_EALIGN, "sys1hip_linear_rope_qkv_bf16: x, w, cos and sin must be 16-byte aligned");
+  const int64_t H = heads * head_dim, N = 3 * H;
+  if (M > (1ll << 30) || N > (1ll << 30) || K > (1ll << 30) || M * H > (1ll << 40))
+    return fail(SYS1HIP_ERANGE, "sys1hip_linear_rope_qkv_bf16: dimension above 2^30");
+  int rc = use_device(c);
+  if (rc) return rc;
+  if (c->forced_kernel >= 0 && kKernels[c->forced_kernel].tn != 64)
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_rope_qkv_bf16: forced kernel %s is not head-aligned",
+                kKernels[c->forced_kernel].name);
+  const Plan p = resolve(c, M, N, K, true);
+  const KernelEntry& e = kKernels[p.kernel];
+  if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
+    return fail(SYS1HIP_ERANGE, "sys1hip_linear_rope_qkv_bf16: more split tiles than stream-K counters");
+  GemmArgs a = {};
+  a.x = reinterpret_cast<const __bf16*>(x);
+  a.w = reinterpret_cast<const __bf16*>(w);
+  a.y = reinterpret_cast<__bf16*>(qkv);
+  a.ws = c->ws;
+  a.counters = c->counters;
+  a.ldx = ldx, a.ldw = ldw, a.ldr = 0, a.ldy = H;
+  a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)N;
+  a.dp_tiles = (int)std::min<int64_t>(p.dp, 1 << 30);
+  a.rope_cos = rope_cos;
+  a.rope_sin = rope_sin;
+  a.pos = positions;
+  a.rope_rows = (int)rope_rows;
+  a.plane = M * H;
+  hipLaunchKernelGGL(e.fn[kEpiRopeQkv], dim3((unsigned)p.grid), dim3(e.threads), 0, c->stream, a);
   HIP_TRY(hipGetLastError());
   return SYS1HIP_OK;
 }

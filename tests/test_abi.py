@@ -119,6 +119,34 @@ def test_gated_output_width_drives_ldy_rule():
     assert _call(M=4, N=64, ldy=30, epi=_lib.EPI_GEGLU) == _lib.EINVAL
 
 
+def _rope(ctx=_ctx, x=_P, ldx=64, w=_P, ldw=64, cos=_P, sin=_P, rows=16, pos=_P, y=_P, M=4, heads=2,
+          dim=64, K=64):
+    L = _lib.load()
+    return L.sys1hip_linear_rope_qkv_bf16(ctx, x, ldx, w, ldw, cos, sin, rows, pos, y, M, heads, dim, K)
+
+
+@pytest.mark.parametrize("kwargs,code", [
+    (dict(ctx=None), _lib.EINVAL),
+    (dict(dim=128), _lib.EINVAL),        # head_dim 64 only
+    (dict(heads=0), _lib.EINVAL),
+    (dict(rows=0), _lib.EINVAL),
+    (dict(M=-1), _lib.EINVAL),
+    (dict(cos=None), _lib.EINVAL),
+    (dict(pos=None), _lib.EINVAL),
+    (dict(ldx=32), _lib.EINVAL),
+    (dict(K=60, ldx=64, ldw=64), _lib.EALIGN),
+    (dict(sin=_P + 4), _lib.EALIGN),
+    (dict(M=(1 << 30) + 1), _lib.ERANGE),
+])
+def test_rope_qkv_rejects_bad_arguments(kwargs, code):
+    rc = _rope(**kwargs)
+    assert rc == code, (kwargs, rc, _lib.load().sys1hip_last_error(None))
+
+
+def test_rope_qkv_empty_batch_is_a_noop():
+    assert _rope(M=0, x=None, y=None, cos=None, sin=None, pos=None) == _lib.OK
+
+
 def test_pack_rejects_bad_arguments():
     L = _lib.load()
     f = L.sys1hip_pack_gated_weight

@@ -42,3 +42,11 @@ def test_cu_seqlens_and_round_trip():
 def test_empty_budget():
     assert batching.draw_lengths(3, 16, 512, 0).size == 0
     assert batching.cu_seqlens([]).tolist() == [0]
+
+
+def test_positions_restart_per_sequence():
+    from sys1_amd.batching import positions
+    np.testing.assert_array_equal(positions([3, 1, 0, 2]), [0, 1, 2, 0, 0, 1])
+    assert positions([]).size == 0
+    p = positions([5, 4])
+    assert p.dtype == np.int32

@@ -215,3 +215,63 @@ def test_oracle_matches_golden_fixtures(orc):
                                s["output"], atol=1e-5, rtol=1e-6)
     r = gold["bf16"]
     np.testing.assert_array_equal(orc.to_bf16_bits(np.array(r["input"], np.float32)), r["bits"])
+
+
+def _transformers_rope(q, k, cos_half, sin_half):
+    """transformers' ModernBERT apply_rotary_pos_emb (rotate-half RoPE, a
+    library routine independent of the reference) on [B, heads, L, dim]."""
+    torch = pytest.importorskip("torch")
+    mb = pytest.importorskip("transformers.models.modernbert.modeling_modernbert")
+    cos = torch.from_numpy(np.concatenate([cos_half, cos_half], -1))[None]
+    sin = torch.from_numpy(np.concatenate([sin_half, sin_half], -1))[None]
+    qo, ko = mb.apply_rotary_pos_emb(torch.from_numpy(q), torch.from_numpy(k), cos, sin)
+    return qo.numpy(), ko.numpy()
+
+
+def test_rope_qkv_reference_fixture_against_transformers(orc):
+    """The reference's own fused-RoPE test (src/archs/modernbert.rs:768-816):
+    qkv (2, 5, 3, 2, 8) from ((i*37 % 127) - 63)/21, cos/sin (5, 4) from
+    i*0.13; the oracle on the packed tokens (position = token % 5) against
+    transformers' rotate-half RoPE and the untouched v."""
+    B, L, heads, dim = 2, 5, 2, 8
+    vals = ((np.arange(480) * 37 % 127).astype(np.float32) - 63.0) / 21.0
+    qkv = vals.reshape(B, L, 3, heads, dim)
+    ang = np.arange(20, dtype=np.float32) * np.float32(0.13)
+    cos_t, sin_t = np.cos(ang).reshape(L, dim // 2), np.sin(ang).reshape(L, dim // 2)
+    packed = qkv.reshape(B * L, 3 * heads * dim)
+    pos = np.arange(B * L) % L
+    out = orc.rope_qkv(packed, cos_t, sin_t, pos, heads, dim)
+    q = np.ascontiguousarray(qkv[:, :, 0].transpose(0, 2, 1, 3))   # [B, heads, L, dim]
+    k = np.ascontiguousarray(qkv[:, :, 1].transpose(0, 2, 1, 3))
+    eq, ek = _transformers_rope(q, k, cos_t, sin_t)
+    got = out.reshape(3, B, L, heads, dim).transpose(0, 1, 3, 2, 4)  # -> [3, B, heads, L, dim]
+    np.testing.assert_allclose(got[0], eq, rtol=0, atol=2e-6)
+    np.testing.assert_allclose(got[1], ek, rtol=0, atol=2e-6)
+    np.testing.assert_array_equal(got[2], qkv[:, :, 2].transpose(0, 2, 1, 3))
+
+
+def test_rope_tables_and_invariants(orc):
+    """Tables against their closed form in float64 (inv_freq[0] = 1, so
+    column 0 is cos/sin of the position itself); RoPE at position 0 is the
+    identity; every rotated (c, c + dim/2) pair keeps its norm; a wrong sign
+    or a swapped half would break the transformers comparison above."""
+    dim, P = 64, 300
+    c, s = orc.rope_tables(160000.0, dim, P)
+    p = np.arange(P, dtype=np.float64)[:, None]
+    inv = 1.0 / 160000.0 ** (np.arange(0, dim, 2, dtype=np.float64) / dim)
+    np.testing.assert_allclose(c, np.cos(p * inv.astype(np.float32)), atol=3e-5)
+    np.testing.assert_allclose(s, np.sin(p * inv.astype(np.float32)), atol=3e-5)
+    np.testing.assert_allclose(c[:, 0], np.cos(np.arange(P)), atol=3e-5)
+    rng = np.random.default_rng(5)
+    heads = 3
+    qkv = rng.standard_normal((7, 3 * heads * dim)).astype(np.float32)
+    out = orc.rope_qkv(qkv, c, s, np.zeros(7, np.int32), heads, dim)
+    np.testing.assert_allclose(out.transpose(1, 0, 2).reshape(7, -1), qkv, atol=1e-6)
+    pos = rng.integers(0, P, 7)
+    out = orc.rope_qkv(qkv, c, s, pos, heads, dim)
+    half = dim // 2
+    for plane in range(2):
+        a = qkv[:, plane * heads * dim:(plane + 1) * heads * dim].reshape(7, heads, 2, half)
+        b = out[plane].reshape(7, heads, 2, half)
+        np.testing.assert_allclose(np.hypot(a[:, :, 0], a[:, :, 1]), np.hypot(b[:, :, 0], b[:, :, 1]),
+                                   rtol=2e-5, atol=1e-5)
