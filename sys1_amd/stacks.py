@@ -87,10 +87,13 @@ def modernbert(hidden: int, intermediate: int, layers: int, name: str) -> StackC
 
 def qwen35(hidden: int, layers: int, heads: int, kv_heads: int, head_dim: int,
            intermediate: int, dn_qk: int, dn_v: int, dn_heads: int, o_in: int,
-           name: str) -> StackConfig:
-    """Hybrid decoder: every 4th layer gated GQA attention, the rest DeltaNet
-    (3:1).  o_in is the o_proj input width (BASELINE states heads*hd*2 for the
-    small config where the reference builds heads*hd; src/archs/qwen35_text.rs:281-285)."""
+           name: str, layer_types: list[str] | None = None) -> StackConfig:
+    """Hybrid decoder: gated GQA attention layers and DeltaNet layers, in the
+    order of `layer_types` ("full_attention" / "linear_attention", the
+    reference's config field, src/archs/qwen35_text.rs:45,905-912), by
+    default every 4th layer attention (3:1).  o_in is the o_proj input width
+    (BASELINE states heads*hd*2 for the small config where the reference
+    builds heads*hd; src/archs/qwen35_text.rs:281-285)."""
     H = hidden
     mlp = [
         Proj("gate_up+swiglu", H, 2 * intermediate, _lib.EPI_SWIGLU, "h", 0, "act"),
@@ -107,7 +110,11 @@ def qwen35(hidden: int, layers: int, heads: int, kv_heads: int, head_dim: int,
         Proj("q_k_v", H, attn_in, _lib.EPI_NONE, "h", 0, "mix"),
         Proj("o_proj", o_in, H, _lib.EPI_RESIDUAL, "mix", 0, "h", resid="h"),
     ] + mlp
-    stack = [list(attention if (i + 1) % 4 == 0 else deltanet) for i in range(layers)]
+    if layer_types is None:
+        layer_types = ["full_attention" if (i + 1) % 4 == 0 else "linear_attention" for i in range(layers)]
+    if len(layer_types) != layers:
+        raise ValueError(f"{len(layer_types)} layer types for {layers} layers")
+    stack = [list(attention if t == "full_attention" else deltanet) for t in layer_types]
     return StackConfig(name, H, stack,
                        f"Qwen3.5 hybrid H={H} x{layers} (3:1 DeltaNet:GQA), in_proj {H}->{dn_in}, "
                        f"out {dn_v}->{H}, qkv {H}->{attn_in}, o {o_in}->{H}, "

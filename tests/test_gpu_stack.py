@@ -307,3 +307,39 @@ def test_row_permutation_is_exact(dev, orc):
         assert torch.equal(lin(x)[perm], lin(x[perm]))
         g = GatedLinear(w, "gelu", device=dev)
         assert torch.equal(g(x)[perm], g(x[perm]))
+
+
+def test_stack_from_safetensors_checkpoint(dev, orc, tmp_path):
+    """A ProjectionStack loaded from a checkpoint in the reference's tensor
+    names equals the stack built from the same tensors, and follows the f32
+    oracle layer (src/archs/modernbert.rs:857-887 with the stand-in)."""
+    st = pytest.importorskip("safetensors.torch")
+    from sys1_amd import weights as W
+    from sys1_amd.stacks import ProjectionStack
+    cfg_json = {"hidden_size": 128, "intermediate_size": 192, "num_hidden_layers": 2,
+                "num_attention_heads": 2}
+    g = torch.Generator().manual_seed(7)
+    t = {}
+    for i in range(2):
+        p = f"model.layers.{i}."
+        t[p + "attn.Wqkv.weight"] = torch.randn(384, 128, generator=g) * 0.05
+        t[p + "attn.Wo.weight"] = torch.randn(128, 128, generator=g) * 0.05
+        t[p + "mlp.Wi.weight"] = torch.randn(384, 128, generator=g) * 0.05
+        t[p + "mlp.Wo.weight"] = torch.randn(128, 192, generator=g) * 0.05
+    path = str(tmp_path / "m.safetensors")
+    st.save_file(t, path)
+    M = 200
+    x = to_gpu_bf16(orc.fill_normal((M, 128), 17), torch)
+    stack = W.load_stack(path, "modernbert", cfg_json, dev, M)
+    out = stack.forward(x, M).clone()
+    ws = [[t[f"model.layers.{i}.{n}.weight"].to(torch.bfloat16).cuda() for n in
+           ("attn.Wqkv", "attn.Wo", "mlp.Wi", "mlp.Wo")] for i in range(2)]
+    direct = ProjectionStack(W.modernbert_config(cfg_json), dev, M, weights=ws).forward(x, M)
+    assert torch.equal(out, direct)
+    h = to_np(x)
+    for i in range(2):
+        f = [to_np(w) for w in ws[i]]
+        h = orc.modernbert_layer_f32(h, *f)
+    rel, _ = parity(to_np(out), h)
+    print(f"[gpu] checkpoint stack vs f32 oracle: rel_fro={rel:.3e}", flush=True)
+    assert rel < CHAIN_TOL

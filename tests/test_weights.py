@@ -1,0 +1,103 @@
+"""Checkpoint loading in the reference's tensor names (host side): tiny
+synthetic safetensors checkpoints, written here, in ModernBERT and Qwen3.5
+naming, some sharded."""
+import json
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+st = pytest.importorskip("safetensors.torch")
+
+from sys1_amd import weights as W  # noqa: E402
+
+MB_CFG = {"hidden_size": 64, "intermediate_size": 96, "num_hidden_layers": 2, "num_attention_heads": 2}
+QW_CFG = {"text_config": {"hidden_size": 64, "num_hidden_layers": 2, "num_attention_heads": 2,
+                          "num_key_value_heads": 1, "head_dim": 16, "intermediate_size": 96,
+                          "linear_num_key_heads": 2, "linear_key_head_dim": 8,
+                          "linear_num_value_heads": 4, "linear_value_head_dim": 8,
+                          "layer_types": ["linear_attention", "full_attention"]}}
+
+
+def _t(g, *shape):
+    return torch.randn(*shape, generator=g)
+
+
+def _modernbert_ckpt(tmp_path, shards=1):
+    g = torch.Generator().manual_seed(0)
+    t = {"model.embeddings.tok_embeddings.weight": _t(g, 10, 64)}
+    for i in range(2):
+        p = f"model.layers.{i}."
+        t[p + "attn.Wqkv.weight"] = _t(g, 192, 64)
+        t[p + "attn.Wo.weight"] = _t(g, 64, 64)
+        t[p + "mlp.Wi.weight"] = _t(g, 192, 64)
+        t[p + "mlp.Wo.weight"] = _t(g, 64, 96)
+        t[p + "mlp_norm.weight"] = _t(g, 64)
+    names = sorted(t)
+    paths = []
+    for s in range(shards):
+        path = str(tmp_path / f"mb-{s}.safetensors")
+        st.save_file({n: t[n].contiguous() for n in names[s::shards]}, path)
+        paths.append(path)
+    return t, paths
+
+
+def test_modernbert_names_and_cast(tmp_path):
+    t, paths = _modernbert_ckpt(tmp_path, shards=2)
+    cfg = W.modernbert_config(MB_CFG)
+    ws = W.read_projection_weights(paths, "modernbert", cfg)
+    for i in range(2):
+        p = f"model.layers.{i}."
+        for got, n in zip(ws[i], ["attn.Wqkv", "attn.Wo", "mlp.Wi", "mlp.Wo"]):
+            assert got.dtype == torch.bfloat16
+            assert torch.equal(got, t[p + n + ".weight"].to(torch.bfloat16))
+
+
+def test_modernbert_shape_and_missing_errors(tmp_path):
+    t, _ = _modernbert_ckpt(tmp_path)
+    bad = dict(t)
+    bad["model.layers.1.attn.Wo.weight"] = torch.zeros(64, 32)
+    path = str(tmp_path / "bad.safetensors")
+    st.save_file(bad, path)
+    with pytest.raises(ValueError, match="attn.Wo"):
+        W.read_projection_weights(path, "modernbert", W.modernbert_config(MB_CFG))
+    del bad["model.layers.1.attn.Wo.weight"]
+    st.save_file(bad, path)
+    with pytest.raises(KeyError):
+        W.read_projection_weights(path, "modernbert", W.modernbert_config(MB_CFG))
+
+
+def test_qwen35_concatenations_follow_layer_types(tmp_path):
+    g = torch.Generator().manual_seed(1)
+    c = QW_CFG["text_config"]
+    kw, vw, nv = 16, 32, 4
+    t = {}
+    p0, p1 = "model.language_model.layers.0.", "model.language_model.layers.1."
+    t[p0 + "linear_attn.in_proj_qkv.weight"] = _t(g, 2 * kw + vw, 64)
+    t[p0 + "linear_attn.in_proj_z.weight"] = _t(g, vw, 64)
+    t[p0 + "linear_attn.in_proj_b.weight"] = _t(g, nv, 64)
+    t[p0 + "linear_attn.in_proj_a.weight"] = _t(g, nv, 64)
+    t[p0 + "linear_attn.out_proj.weight"] = _t(g, 64, vw)
+    t[p1 + "self_attn.q_proj.weight"] = _t(g, 2 * 2 * 16, 64)
+    t[p1 + "self_attn.k_proj.weight"] = _t(g, 16, 64)
+    t[p1 + "self_attn.v_proj.weight"] = _t(g, 16, 64)
+    t[p1 + "self_attn.o_proj.weight"] = _t(g, 64, 2 * 16)
+    for p in (p0, p1):
+        t[p + "mlp.gate_proj.weight"] = _t(g, 96, 64)
+        t[p + "mlp.up_proj.weight"] = _t(g, 96, 64)
+        t[p + "mlp.down_proj.weight"] = _t(g, 64, 96)
+    path = str(tmp_path / "qwen.safetensors")
+    st.save_file(t, path)
+    cfgpath = tmp_path / "config.json"
+    cfgpath.write_text(json.dumps(QW_CFG))
+    cfg = W.qwen35_config(json.loads(cfgpath.read_text()))
+    assert [l[0].name for l in cfg.layers] == ["in_proj_qkvzba", "q_k_v"]
+    ws = W.read_projection_weights(path, "qwen35", cfg)
+    b = lambda n: t[n].to(torch.bfloat16)
+    assert torch.equal(ws[0][0], torch.cat([b(p0 + f"linear_attn.in_proj_{n}.weight") for n in ("qkv", "z", "b", "a")]))
+    assert torch.equal(ws[0][1], b(p0 + "linear_attn.out_proj.weight"))
+    assert torch.equal(ws[1][0], torch.cat([b(p1 + f"self_attn.{n}_proj.weight") for n in "qkv"]))
+    assert torch.equal(ws[1][1], b(p1 + "self_attn.o_proj.weight"))
+    for i, p in enumerate((p0, p1)):
+        assert torch.equal(ws[i][2], torch.cat([b(p + "mlp.gate_proj.weight"), b(p + "mlp.up_proj.weight")]))
+        assert torch.equal(ws[i][3], b(p + "mlp.down_proj.weight"))
