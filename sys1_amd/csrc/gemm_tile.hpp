@@ -29,7 +29,7 @@
 //          Fragments are double-buffered in registers across k-steps, and the
 //          last k-step's MFMAs run after the barrier, overlapping the next
 //          k-tile's first LDS reads; the freed stage's refill is issued
-//          behind them.
+//          behind them (spread between them with one workgroup per CU).
 // Epilogue: straight from registers: lane pairs (l, l+32) exchange halves
 //          with v_permlane32_swap so that every lane stores (and reads the
 //          residual as) 16 contiguous bytes; no LDS, so all of it goes to
@@ -47,6 +47,8 @@
 //          to it and re-arms the counter.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace sys1 {
@@ -62,9 +64,18 @@ typedef __attribute__((address_space(3))) void lds_void;
 // kOutOfRange fall outside it and read as zeros.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr unsigned kOutOfRange = 0x80000000u;
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7ffffff0,
-                                           0x00020000);
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes = 0x7ffffff0) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+// The same from values the caller knows to be wave-uniform, moved to SGPRs
+// explicitly: a descriptor the compiler cannot prove uniform is otherwise
+// consumed through a readfirstlane loop around every load.
+__device__ __forceinline__ rsrc_t make_rsrc_uniform(const void* base, int bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  return make_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo),
+                   __builtin_amdgcn_readfirstlane(bytes));
 }
 
 // Asynchronous 16-byte-per-lane copy global -> LDS: lane i's 16 bytes (from
@@ -285,29 +296,45 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
   Segment isg = walk.first_segment();
   int is_kt = isg.kt0;
   set_offsets(isg);
-  auto issue = [&](int stage) {  // issue the cursor's k-tile, then advance the cursor
+  // A refill of one stage from the cursor's k-tile, prepared once (scalar
+  // descriptors, stage base, K-tail extent); dma_one(r, i) issues its
+  // instruction i and issue_advance() then moves the cursor on, so that the
+  // refill can be spread between MFMAs (mma_dma below).  A refill that is
+  // not live gets descriptors of zero size: its instructions read zeros into
+  // a stage that is never read again (the end of the stream), so the main
+  // loop issues the same instruction sequence every k-tile.
+  struct Refill {
+    rsrc_t xr, wr;
+    char* base;
+    int kleft;  // valid K elements in the k-tile
+  };
+  auto refill_at = [&](int stage, bool live) {
+    Refill r;
     const int m0 = isg.tm * BM, n0 = isg.tn * BN;
-    char* base = lds + stage * S::kStageBytes;
-    const rsrc_t xr = make_rsrc(reinterpret_cast<const char*>(a.x + (int64_t)m0 * a.ldx) + is_kt * BK * 2);
-    const rsrc_t wr = make_rsrc(reinterpret_cast<const char*>(a.w + (int64_t)n0 * a.ldw) + is_kt * BK * 2);
-    const int kleft = a.K - is_kt * BK;  // valid K elements in this k-tile
-    if (kleft >= BK) {
-#pragma unroll
-      for (int i = 0; i < S::kDma; ++i)
-        dma16(i < kXDma ? xr : wr, src_off[i], (lds_void*)(base + (i * S::kWaves + wave) * 1024));
-    } else {
-#pragma unroll
-      for (int i = 0; i < S::kDma; ++i) {
-        const int c = lpos ^ lds_swz<BK>(dma_row(i));
-        const unsigned off = c * 8 >= kleft ? kOutOfRange : src_off[i];
-        dma16(i < kXDma ? xr : wr, off, (lds_void*)(base + (i * S::kWaves + wave) * 1024));
-      }
-    }
+    const int bytes = live ? 0x7ffffff0 : 0;
+    r.base = lds + stage * S::kStageBytes;
+    r.xr = make_rsrc_uniform(reinterpret_cast<const char*>(a.x + (int64_t)m0 * a.ldx) + is_kt * BK * 2, bytes);
+    r.wr = make_rsrc_uniform(reinterpret_cast<const char*>(a.w + (int64_t)n0 * a.ldw) + is_kt * BK * 2, bytes);
+    r.kleft = a.K - is_kt * BK;
+    return r;
+  };
+  auto dma_one = [&](const Refill& r, int i) {
+    unsigned off = src_off[i];
+    if (r.kleft < BK && (lpos ^ lds_swz<BK>(dma_row(i))) * 8 >= r.kleft) off = kOutOfRange;
+    dma16(i < kXDma ? r.xr : r.wr, off, (lds_void*)(r.base + (i * S::kWaves + wave) * 1024));
+  };
+  auto issue_advance = [&]() {
     if (++is_kt == isg.kt1) {
       isg = walk.next_segment(isg);
       is_kt = isg.kt0;
       set_offsets(isg);
     }
+  };
+  auto issue = [&](int stage) {  // issue the cursor's k-tile, then advance the cursor
+    const Refill r = refill_at(stage, true);
+#pragma unroll
+    for (int i = 0; i < S::kDma; ++i) dma_one(r, i);
+    issue_advance();
   };
 
   // ---- fragment addressing (byte offsets within a stage): lane reads row
@@ -359,6 +386,24 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
     for (int i = 0; i < S::FN; ++i)
 #pragma unroll
       for (int j = 0; j < S::FM; ++j) acc[i][j] = mfma32(f.w[i], f.x[j], acc[i][j]);
+  };
+  // The same MFMAs with DMA instructions [I0, I0 + N) of refill `r` spread
+  // evenly between them (after MFMA q go instructions I0 + q*N/Q ..
+  // I0 + (q+1)*N/Q - 1, Q MFMAs in all), so that the load path drains while
+  // the matrix unit works.
+  auto mma_dma = [&](const Frags& f, const Refill& r, auto i0c, auto nc) {
+    constexpr int I0 = decltype(i0c)::value, N = decltype(nc)::value;
+    constexpr int Q = S::FN * S::FM;
+#pragma unroll
+    for (int i = 0; i < S::FN; ++i)
+#pragma unroll
+      for (int j = 0; j < S::FM; ++j) {
+        const int q = i * S::FM + j;
+        acc[i][j] = mfma32(f.w[i], f.x[j], acc[i][j]);
+#pragma unroll
+        for (int d = I0 + q * N / Q; d < I0 + (q + 1) * N / Q; ++d) dma_one(r, d);
+        __builtin_amdgcn_sched_barrier(0);
+      }
   };
 
   // ---- epilogue of one tile, straight from registers.  A lane's
@@ -634,25 +679,49 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
     // that stall overlaps matrix work instead of delaying it.
     const int freed = stage;
     stage = stage + 1 == STAGES ? 0 : stage + 1;
-    if constexpr (kDeep) {
+    // One workgroup per CU (OCC == 1): the refill's instructions go between
+    // the MFMAs that follow the barrier.  With two workgroups per CU the
+    // other workgroup's MFMAs cover the refill, and one burst after the
+    // first MFMA group measured faster.
+    using std::integral_constant;
+    constexpr bool kSpread = OCC == 1;
+    const Refill r = refill_at(freed, s + STAGES < steps);
+    auto refill_all = [&]() {
+#pragma unroll
+      for (int i = 0; i < S::kDma; ++i) dma_one(r, i);
+    };
+    if constexpr (kDeep && kSpread) {
+      constexpr int kHalf = S::kDma / 2;
+      if (s + 1 < steps) {
+        read(fr[0], stage, 0);
+        read(fr[1], stage, 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mma_dma(fr[2], r, integral_constant<int, 0>(), integral_constant<int, kHalf>());
+      mma_dma(fr[3], r, integral_constant<int, kHalf>(), integral_constant<int, S::kDma - kHalf>());
+    } else if constexpr (kDeep) {
       if (s + 1 < steps) read(fr[0], stage, 0);
       __builtin_amdgcn_sched_barrier(0);
       mma(fr[2]);
       __builtin_amdgcn_sched_barrier(0);
-      if (s + STAGES < steps) issue(freed);
+      refill_all();
       __builtin_amdgcn_sched_barrier(0);
       if (s + 1 < steps) read(fr[1], stage, 1);
       __builtin_amdgcn_sched_barrier(0);
       mma(fr[3]);
+    } else if constexpr (kSpread) {
+      if (s + 1 < steps) read(fr[0], stage, 0);
       __builtin_amdgcn_sched_barrier(0);
+      mma_dma(fr[(S::KS - 1) % 2], r, integral_constant<int, 0>(), integral_constant<int, S::kDma>());
     } else {
       if (s + 1 < steps) read(fr[0], stage, 0);
       __builtin_amdgcn_sched_barrier(0);
       mma(fr[(S::KS - 1) % 2]);
       __builtin_amdgcn_sched_barrier(0);
-      if (s + STAGES < steps) issue(freed);
-      __builtin_amdgcn_sched_barrier(0);
+      refill_all();
     }
+    if (s + STAGES < steps) issue_advance();
+    __builtin_amdgcn_sched_barrier(0);
     if (++ckt == csg.kt1) {
       if constexpr (STREAMK) {
         if (walk.complete(csg) || finish_partial(csg)) epilogue(csg.tm * BM, csg.tn * BN);
@@ -666,6 +735,7 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
       }
     }
   }
+  vm_wait<0>();  // the zero-size refills of the last k-tiles write LDS too
 }
 
 }  // namespace sys1

@@ -268,6 +268,30 @@ def test_tile_kernel_small_forced_grid(dev, orc):
         dev.set_kernel(-1)
 
 
+@pytest.mark.parametrize("kname", [n for n in __import__("sys1_amd").kernel_names()
+                                   if not n.startswith("stream_")])
+def test_tile_kernels_short_k_and_small_grids(dev, orc, kname):
+    """Streams of 1..6 k-tiles per tile and 1..n tiles per workgroup: the
+    pipeline prologue and refill cursors at every stream length."""
+    from sys1_amd import kernel_names
+    from sys1_amd.linear import Linear
+    dev.set_kernel(kernel_names().index(kname))
+    try:
+        for K in (40, 72, 136, 328):
+            M, N = 520, 520
+            x, w = _inputs(orc, M, N, K, 43 + K)
+            proj = orc.linear_f64(orc.round_bf16(x), orc.round_bf16(w)).astype(np.float32)
+            lin = Linear(to_gpu_bf16(w, torch), device=dev)
+            xg = to_gpu_bf16(x, torch)
+            for g in (0, 1, 3, 9):
+                dev.set_grid(g)
+                print(f"[gpu] {kname} K={K} grid={g} {dev.query_kernel(M, N, K)[1]}", flush=True)
+                _check_close_to_rounded(orc, to_np(lin(xg)), proj, f"{kname} K={K} grid={g}")
+    finally:
+        dev.set_grid(0)
+        dev.set_kernel(-1)
+
+
 def test_python_errors(dev, orc):
     from sys1_amd import Sys1HipError
     from sys1_amd.linear import GatedLinear, Linear
