@@ -149,6 +149,42 @@ SYS1HIP_API int sys1hip_linear_rope_qkv_bf16(void* ctx, const uint16_t* x, int64
                                              const int32_t* positions, uint16_t* qkv, int64_t M,
                                              int64_t heads, int64_t head_dim, int64_t K);
 
+/* Pre-norm projections: the norm that precedes a projection in the
+ * reference's layers, fused into it.
+ *   SYS1HIP_NORM_LAYER  bias-free LayerNorm, ModernBERT attn_norm / mlp_norm
+ *                       (src/archs/modernbert.rs:1005-1034, used at :865-868,884)
+ *   SYS1HIP_NORM_RMS    RMSNorm with alpha = 1 + weight, Qwen3.5
+ *                       input_layernorm / post_attention_layernorm
+ *                       (src/archs/qwen35_text.rs:178-203, used at :933,939)
+ * Replaces `x.apply(&norm)?.apply(&linear)` at those sites: the norm weight
+ * is folded into the projection weight once at load (fold_norm_weight), the
+ * call computes per-row statistics of x and then the projection of the raw
+ * x with the normalisation applied to the accumulators. */
+#define SYS1HIP_NORM_LAYER 1
+#define SYS1HIP_NORM_RMS 2
+
+/* Load time: w_folded[n,k] = bf16(w[n,k] * a_k), a = gamma (LayerNorm) or
+ * 1 + gamma (RMSNorm), gamma f32 [K]; for LayerNorm also colsum[n] = sum_k
+ * w_folded[n,k] (f32 [N], 16-byte aligned; may be null for RMSNorm).  For a
+ * gated projection pass the packed weight (sys1hip_pack_gated_weight first):
+ * the fold is per row, so colsum then follows the packed row order.
+ * w_folded may alias w. */
+SYS1HIP_API int sys1hip_fold_norm_weight(void* ctx, const uint16_t* w, const float* gamma,
+                                         int32_t norm, uint16_t* w_folded, float* colsum,
+                                         int64_t N, int64_t K);
+
+/* y[M,Nout] = epilogue(norm(x) . W^T) with W given folded:
+ *   LayerNorm: y = epi(r_m (x_m . w_folded_n - mu_m colsum_n)),
+ *   RMSNorm:   y = epi(r_m (x_m . w_folded_n)),
+ * mu_m, r_m = mean and 1/sqrt(var + eps) of row m of x (f32; RMSNorm:
+ * var = mean of squares), computed by the call.  epilogue: SYS1HIP_EPI_NONE,
+ * or SYS1HIP_EPI_GEGLU with LayerNorm (ModernBERT Wi), SYS1HIP_EPI_SWIGLU with
+ * RMSNorm (Qwen gate/up).  M up to 2^20 rows per call. */
+SYS1HIP_API int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx,
+                                         const uint16_t* w_folded, int64_t ldw, const float* colsum,
+                                         int32_t norm, float eps, uint16_t* y, int64_t ldy,
+                                         int64_t M, int64_t N, int64_t K, int32_t epilogue);
+
 /* Tuning and test knob, no counterpart in the reference: force how many
  * tiles a stream-K kernel runs whole before its stream phase, for every
  * later call on this context (-1 = automatic; clamped to the tile count).

@@ -167,6 +167,20 @@ ORC_EXPORT void orc_layer_norm(const float* x, int64_t ldx, const float* g, cons
     }
 }
 
+/* RMSNorm with alpha = 1 + w (src/archs/qwen35_text.rs:178-203): in f32,
+ * variance = mean(x^2), scale = 1 / sqrt(variance + eps), y = x * scale *
+ * alpha.  Mean of squares accumulated in double. */
+ORC_EXPORT void orc_rms_norm(const float* x, int64_t ldx, const float* w, float eps, float* y,
+                             int64_t ldy, int64_t M, int64_t H) {
+    for (int64_t m = 0; m < M; ++m) {
+        double ss = 0.0;
+        for (int64_t h = 0; h < H; ++h) ss += (double)x[m * ldx + h] * x[m * ldx + h];
+        const float var = (float)(ss / (double)H);
+        const float scale = 1.0f / sqrtf(var + eps);
+        for (int64_t h = 0; h < H; ++h) y[m * ldy + h] = x[m * ldx + h] * scale * (1.0f + w[h]);
+    }
+}
+
 /* Argmax with ties broken towards the lowest index (src/models/laya.rs:909-916:
  * max_by with total_cmp, then reversed index order). */
 ORC_EXPORT int64_t orc_argmax(const float* v, int64_t n) {

@@ -46,6 +46,7 @@ def lib():
         L.orc_swiglu.argtypes = [_f32p, _i64, _f32p, _i64, _f32p, _i64, _i64, _i64]
         L.orc_add_inplace.argtypes = [_f32p, _i64, _f32p, _i64, _i64, _i64]
         L.orc_layer_norm.argtypes = [_f32p, _i64, _f32p, _f32p, ctypes.c_float, _f32p, _i64, _i64, _i64]
+        L.orc_rms_norm.argtypes = [_f32p, _i64, _f32p, ctypes.c_float, _f32p, _i64, _i64, _i64]
         L.orc_argmax.argtypes = [_f32p, _i64]
         L.orc_argmax.restype = _i64
         L.orc_round_bf16.argtypes = [ctypes.c_float]
@@ -157,6 +158,30 @@ def layer_norm(x, weight, bias, eps=1e-5) -> np.ndarray:
     b = _f32(bias) if bias is not None else None
     lib().orc_layer_norm(_p(x2), H, _p(g), _p(b) if b is not None else None, eps, _p(y), H,
                          x2.shape[0], H)
+    return y.reshape(x.shape)
+
+
+def layer_norm_bf16(x, weight, eps=1e-5) -> np.ndarray:
+    """ModernBERT's bias-free LayerNorm on bf16 activations
+    (src/archs/modernbert.rs:1005-1034, `LayerNorm::new_no_bias`), as
+    candle-nn 0.11.0's LayerNorm::forward computes it for a bf16 input
+    without bias: in f32, centre by the mean, divide by sqrt(mean of squared
+    deviations + eps), cast the normalised value to bf16, then multiply by
+    the weight in bf16 (rounded)."""
+    H = _f32(x).shape[-1]
+    normed = round_bf16(layer_norm(x, np.ones(H, np.float32), None, eps))
+    return round_bf16(normed * round_bf16(_f32(weight)))
+
+
+def rms_norm(x, weight, eps=1e-6) -> np.ndarray:
+    """Qwen3.5 RMSNorm, f32 result before the cast back to the input dtype
+    (src/archs/qwen35_text.rs:178-203; alpha = 1 + weight)."""
+    x = _f32(x)
+    H = x.shape[-1]
+    x2 = x.reshape(-1, H)
+    y = np.empty_like(x2)
+    w = _f32(weight)
+    lib().orc_rms_norm(_p(x2), H, _p(w), eps, _p(y), H, x2.shape[0], H)
     return y.reshape(x.shape)
 
 

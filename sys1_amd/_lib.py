@@ -20,6 +20,10 @@ EPI_RESIDUAL = 8
 EPI_GELU = 16
 GATE_GROUP = 16
 
+# Pre-norm kinds (include/sys1hip.h).
+NORM_LAYER = 1
+NORM_RMS = 2
+
 OK = 0
 EINVAL = -22
 EALIGN = -14
@@ -32,7 +36,8 @@ EXPORTS = (
     "sys1hip_sync", "sys1hip_last_error", "sys1hip_linear_bf16",
     "sys1hip_pack_gated_weight", "sys1hip_query_kernel", "sys1hip_set_kernel",
     "sys1hip_kernel_count", "sys1hip_kernel_name", "sys1hip_set_grid",
-    "sys1hip_set_dp_tiles", "sys1hip_linear_rope_qkv_bf16",
+    "sys1hip_set_dp_tiles", "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
+    "sys1hip_norm_linear_bf16",
 )
 
 
@@ -72,14 +77,17 @@ def load() -> ctypes.CDLL:
     L.sys1hip_set_grid.argtypes = [vp, i32]
     L.sys1hip_set_dp_tiles.argtypes = [vp, i32]
     L.sys1hip_linear_rope_qkv_bf16.argtypes = [vp, vp, i64, vp, i64, vp, vp, i64, vp, vp, i64, i64, i64, i64]
+    L.sys1hip_fold_norm_weight.argtypes = [vp, vp, vp, i32, vp, vp, i64, i64]
+    L.sys1hip_norm_linear_bf16.argtypes = [vp, vp, i64, vp, i64, vp, i32, ctypes.c_float, vp, i64,
+                                           i64, i64, i64, i32]
     L.sys1hip_kernel_count.argtypes = []
     L.sys1hip_kernel_name.argtypes = [i32]
     L.sys1hip_kernel_name.restype = ctypes.c_char_p
     for name in ("sys1hip_init", "sys1hip_destroy", "sys1hip_set_stream", "sys1hip_sync",
                  "sys1hip_linear_bf16", "sys1hip_pack_gated_weight", "sys1hip_query_kernel",
                  "sys1hip_set_kernel", "sys1hip_set_grid", "sys1hip_set_dp_tiles",
-                 "sys1hip_linear_rope_qkv_bf16",
-                 "sys1hip_kernel_count"):
+                 "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
+                 "sys1hip_norm_linear_bf16", "sys1hip_kernel_count"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

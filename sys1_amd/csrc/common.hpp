@@ -27,10 +27,34 @@ enum Epi : int {
   kEpiBiasGelu = 5,
   kEpiBiasResidual = 6,
   kEpiRopeQkv = 7,   // Wqkv: RoPE on q and k, q/k/v written as three planes
-  kEpiCount = 8,
+  // Pre-norm projections (the norm's weight folded into w; per-row mean and
+  // reciprocal deviation in `stats`, per-row sums of the folded w in
+  // `colsum`): y = epi(r_m (acc - mu_m c_n)) for LayerNorm, epi(r_m acc) for
+  // RMSNorm, with epi the base epilogue named.
+  kEpiNormLn = 8,
+  kEpiNormLnGeglu = 9,
+  kEpiNormRms = 10,
+  kEpiNormRmsSwiglu = 11,
+  kEpiCount = 12,
 };
 
-__host__ __device__ constexpr bool epi_gated(int e) { return e == kEpiGeglu || e == kEpiSwiglu; }
+enum NormKind : int { kNormNone = 0, kNormLayer = 1, kNormRms = 2 };
+
+__host__ __device__ constexpr int epi_norm(int e) {
+  return e == kEpiNormLn || e == kEpiNormLnGeglu ? kNormLayer
+         : e == kEpiNormRms || e == kEpiNormRmsSwiglu ? kNormRms
+                                                      : kNormNone;
+}
+// The epilogue applied after the normalisation.
+__host__ __device__ constexpr int epi_base(int e) {
+  return e == kEpiNormLn || e == kEpiNormRms ? kEpiNone
+         : e == kEpiNormLnGeglu              ? kEpiGeglu
+         : e == kEpiNormRmsSwiglu            ? kEpiSwiglu
+                                             : e;
+}
+__host__ __device__ constexpr bool epi_gated(int e) {
+  return epi_base(e) == kEpiGeglu || epi_base(e) == kEpiSwiglu;
+}
 
 // f32 -> bf16 with round-to-nearest-even (clang lowers this to the gfx950
 // hardware conversion), and back.
@@ -118,6 +142,10 @@ struct GemmArgs {
   const int* pos;
   int rope_rows;        // table rows: positions are clamped into [0, rope_rows)
   int64_t plane;
+  // Pre-norm epilogues: stats[2m] = mean (0 for RMSNorm), stats[2m+1] =
+  // 1/sqrt(var + eps) of input row m; colsum[n] = sum_k w[n, k] (LayerNorm).
+  const float* stats;
+  const float* colsum;
 };
 
 // Map the hardware workgroup id to a logical tile id so that each XCD gets a

@@ -423,16 +423,61 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
     const i32x4 v = {(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
     return __builtin_bit_cast(bf16x8, v);
   };
+  // Pre-norm epilogues scale the accumulators of row m first: r_m (acc -
+  // mu_m c_n) for LayerNorm, r_m acc for RMSNorm (the norm weight is folded
+  // into w, c_n = sum_k of folded row n); then the base epilogue E runs.
+  constexpr int E = epi_base(EPI);
+  constexpr int NORM = epi_norm(EPI);
+  // All of a tile's row statistics and column sums are loaded before any of
+  // them is used, so the epilogue waits for one round trip, not one per
+  // block.
+  auto normalize_tile = [&](int m0, int n0) {
+    float mu[S::FM], rs[S::FM];
+#pragma unroll
+    for (int j = 0; j < S::FM; ++j) {
+      const int m = min(m0 + wm * S::TM + j * 32 + frow, a.M - 1);
+      mu[j] = a.stats[2 * (int64_t)m];
+      rs[j] = a.stats[2 * (int64_t)m + 1];
+    }
+    f32x4 cs[S::FN][4];
+    if constexpr (NORM == kNormLayer) {
+#pragma unroll
+      for (int i = 0; i < S::FN; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + wn * S::TN + i * 32 + 8 * g + 4 * fk;  // w row of register 4g + e: n + e
+          if (n + 3 < a.N) {
+            cs[i][g] = *reinterpret_cast<const f32x4*>(a.colsum + n);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cs[i][g][e] = a.colsum[min(n + e, a.N - 1)];
+          }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < S::FN; ++i)
+#pragma unroll
+      for (int j = 0; j < S::FM; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float v = acc[i][j][4 * g + e];
+            if constexpr (NORM == kNormLayer) acc[i][j][4 * g + e] = rs[j] * (v - mu[j] * cs[i][g][e]);
+            else acc[i][j][4 * g + e] = v * rs[j];
+          }
+  };
   auto epilogue = [&](int m0, int n0) {
+    if constexpr (NORM != kNormNone) normalize_tile(m0, n0);
     const int h = fk;
-    const int out_n0 = epi_gated(EPI) ? (n0 + wn * S::TN) / 2 : n0 + wn * S::TN;
+    const int out_n0 = epi_gated(E) ? (n0 + wn * S::TN) / 2 : n0 + wn * S::TN;
 #pragma unroll
     for (int j = 0; j < S::FM; ++j) {
       const int m = m0 + wm * S::TM + j * 32 + frow;
       const bool row_ok = m < a.M;
 #pragma unroll
       for (int i = 0; i < S::FN; ++i) {
-        if constexpr (EPI == kEpiRopeQkv) {
+        if constexpr (E == kEpiRopeQkv) {
           // Blocks i (even) and i+1 are the two halves of one 64-wide head
           // (the plan guarantees 64-wide, head-aligned wave columns), so a
           // lane holds columns c and c+32 of the same token: the rotation
@@ -483,7 +528,7 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
               }
             }
           }
-        } else if constexpr (epi_gated(EPI)) {
+        } else if constexpr (epi_gated(E)) {
           // A 32-row block of the packed weight is 16 gate rows then the 16
           // up rows of the same 16 output columns: registers 4g+e (g = 0, 1)
           // hold gate rows, 4(g+2)+e the matching up rows.
@@ -492,7 +537,7 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
           for (int g = 0; g < 2; ++g)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              o[g][e] = to_bf16(epi_gate<EPI>(acc[i][j][4 * g + e], acc[i][j][4 * (g + 2) + e]));
+              o[g][e] = to_bf16(epi_gate<E>(acc[i][j][4 * g + e], acc[i][j][4 * (g + 2) + e]));
           const bf16x8 v = pair16(o[0], o[1]);
           const int n = out_n0 + i * 16 + 8 * h;
           if (row_ok && n < a.Nout) store8(a.y + (int64_t)m * a.ldy + n, v, a.Nout - n);
@@ -508,15 +553,15 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
             const int n = out_n0 + i * 32 + 16 * gp + 8 * h;
             if (row_ok && n < a.Nout) {
               const int valid = a.Nout - n;
-              if constexpr (EPI != kEpiNone) {
+              if constexpr (E != kEpiNone) {
                 float b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-                if constexpr (epi_has_bias<EPI>()) load8(a.bias + n, b, valid);
+                if constexpr (epi_has_bias<E>()) load8(a.bias + n, b, valid);
                 float r[8];
-                if constexpr (epi_has_resid<EPI>()) load8(a.resid + (int64_t)m * a.ldr + n, r, valid);
+                if constexpr (epi_has_resid<E>()) load8(a.resid + (int64_t)m * a.ldr + n, r, valid);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                  float t = epi_pre<EPI>(to_f32(v[e]), b[e]);
-                  if constexpr (epi_has_resid<EPI>()) t = round_bf16(t + r[e]);
+                  float t = epi_pre<E>(to_f32(v[e]), b[e]);
+                  if constexpr (epi_has_resid<E>()) t = round_bf16(t + r[e]);
                   v[e] = to_bf16(t);
                 }
               }

@@ -12,6 +12,7 @@
 
 #include "common.hpp"
 #include "gemm_tile.hpp"
+#include "norm.hpp"
 
 using namespace sys1;
 
@@ -20,6 +21,7 @@ namespace {
 constexpr int kVersion = 100;                        // 0.1.0
 constexpr size_t kWorkspaceBytes = 64ull << 20;      // stream-K partials
 constexpr int kCounterSlots = 1 << 16;               // stream-K arrival counters (tile x wave)
+constexpr int64_t kNormRows = 1 << 20;               // rows of one pre-norm call (row statistics)
 
 thread_local std::string g_last_error;
 
@@ -46,6 +48,7 @@ struct Context {
   hipStream_t stream = nullptr;
   float* ws = nullptr;
   unsigned* counters = nullptr;
+  float* stats = nullptr;  // pre-norm row statistics, kNormRows x (mean, 1/std)
   int forced_kernel = -1;
   int forced_grid = 0;
   int forced_dp = -1;
@@ -77,7 +80,11 @@ constexpr KernelEntry tile_entry(const char* name, float eff) {
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 4>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 5>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 6>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 7>}};
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 7>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 8>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 9>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 10>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 11>}};
 }
 
 // Output-tile shapes.  The first group serves large M (MFMA-bound); the
@@ -291,9 +298,11 @@ int sys1hip_init(int device, void** out) {
   if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess ||
       hipMalloc(&c->ws, kWorkspaceBytes) != hipSuccess ||
       hipMalloc(&c->counters, kCounterSlots * sizeof(unsigned)) != hipSuccess ||
+      hipMalloc(&c->stats, kNormRows * 2 * sizeof(float)) != hipSuccess ||
       hipMemsetAsync(c->counters, 0, kCounterSlots * sizeof(unsigned), c->own) != hipSuccess ||
       hipStreamSynchronize(c->own) != hipSuccess) {
     const char* msg = hipGetErrorString(hipGetLastError());
+    if (c->stats) (void)hipFree(c->stats);
     if (c->counters) (void)hipFree(c->counters);
     if (c->ws) (void)hipFree(c->ws);
     if (c->own) (void)hipStreamDestroy(c->own);
@@ -311,6 +320,7 @@ int sys1hip_destroy(void* ctx) {
   int rc = use_device(c);
   if (rc) return rc;
   HIP_TRY(hipStreamSynchronize(c->stream));
+  (void)hipFree(c->stats);
   (void)hipFree(c->counters);
   (void)hipFree(c->ws);
   (void)hipStreamDestroy(c->own);
@@ -488,6 +498,106 @@ int sys1hip_linear_rope_qkv_bf16(void* ctx, const uint16_t* x, int64_t ldx, cons
   a.rope_rows = (int)rope_rows;
   a.plane = M * H;
   hipLaunchKernelGGL(e.fn[kEpiRopeQkv], dim3((unsigned)p.grid), dim3(e.threads), 0, c->stream, a);
+  HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+
+int sys1hip_fold_norm_weight(void* ctx, const uint16_t* w, const float* gamma, int32_t norm,
+                             uint16_t* w_folded, float* colsum, int64_t N, int64_t K) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_fold_norm_weight: null context");
+  Context* c = static_cast<Context*>(ctx);
+  if (norm != SYS1HIP_NORM_LAYER && norm != SYS1HIP_NORM_RMS)
+    return fail(SYS1HIP_EINVAL, "sys1hip_fold_norm_weight: unknown norm %d", norm);
+  if (N <= 0 || K <= 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_fold_norm_weight: bad shape N=%lld K=%lld", (long long)N,
+                (long long)K);
+  if (!w || !gamma || !w_folded || (norm == SYS1HIP_NORM_LAYER && !colsum))
+    return fail(SYS1HIP_EINVAL, "sys1hip_fold_norm_weight: null pointer");
+  if (K % 8) return fail(SYS1HIP_EALIGN, "sys1hip_fold_norm_weight: K must be a multiple of 8");
+  if (!aligned16(w) || !aligned16(w_folded) || !aligned16(gamma))
+    return fail(SYS1HIP_EALIGN, "sys1hip_fold_norm_weight: w, w_folded and gamma must be 16-byte aligned");
+  if (N > (1ll << 30) || K > (1ll << 30))
+    return fail(SYS1HIP_ERANGE, "sys1hip_fold_norm_weight: dimension above 2^30");
+  int rc = use_device(c);
+  if (rc) return rc;
+  const unsigned blocks = (unsigned)cdiv(N, 4);
+  const auto* wb = reinterpret_cast<const __bf16*>(w);
+  auto* ob = reinterpret_cast<__bf16*>(w_folded);
+  if (norm == SYS1HIP_NORM_LAYER)
+    hipLaunchKernelGGL(fold_norm_kernel<kNormLayer>, dim3(blocks), dim3(256), 0, c->stream, wb, gamma, ob,
+                       colsum, (int)N, (int)K);
+  else
+    hipLaunchKernelGGL(fold_norm_kernel<kNormRms>, dim3(blocks), dim3(256), 0, c->stream, wb, gamma, ob,
+                       colsum, (int)N, (int)K);
+  HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+
+int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_t* w_folded,
+                             int64_t ldw, const float* colsum, int32_t norm, float eps, uint16_t* y,
+                             int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t epilogue) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: null context");
+  Context* c = static_cast<Context*>(ctx);
+  int epi = -1;
+  if (norm == SYS1HIP_NORM_LAYER && epilogue == SYS1HIP_EPI_NONE) epi = kEpiNormLn;
+  if (norm == SYS1HIP_NORM_LAYER && epilogue == SYS1HIP_EPI_GEGLU) epi = kEpiNormLnGeglu;
+  if (norm == SYS1HIP_NORM_RMS && epilogue == SYS1HIP_EPI_NONE) epi = kEpiNormRms;
+  if (norm == SYS1HIP_NORM_RMS && epilogue == SYS1HIP_EPI_SWIGLU) epi = kEpiNormRmsSwiglu;
+  if (epi < 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: unsupported norm %d with epilogue flags %d",
+                norm, epilogue);
+  if (M < 0 || N <= 0 || K <= 0 || !(eps >= 0.0f))
+    return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: bad shape M=%lld N=%lld K=%lld or eps",
+                (long long)M, (long long)N, (long long)K);
+  const bool gated = epi_gated(epi);
+  if (gated && (N % (2 * SYS1HIP_GATE_GROUP)) != 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: gated epilogue needs N %% 32 == 0 (N=%lld)",
+                (long long)N);
+  const int64_t nout = gated ? N / 2 : N;
+  if (M == 0) return SYS1HIP_OK;
+  if (!x || !w_folded || !y || (norm == SYS1HIP_NORM_LAYER && !colsum))
+    return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: null pointer");
+  if (ldx < K || ldw < K || ldy < nout)
+    return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: leading dimension too small");
+  if (K % 8 || ldx % 8 || ldw % 8)
+    return fail(SYS1HIP_EALIGN, "sys1hip_norm_linear_bf16: K, ldx and ldw must be multiples of 8");
+  if (!aligned16(x) || !aligned16(w_folded) || (colsum && !aligned16(colsum)))
+    return fail(SYS1HIP_EALIGN, "sys1hip_norm_linear_bf16: x, w_folded and colsum must be 16-byte aligned");
+  if (M > kNormRows)
+    return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: M=%lld above the %lld rows of one call",
+                (long long)M, (long long)kNormRows);
+  if (N > (1ll << 30) || K > (1ll << 30))
+    return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: dimension above 2^30");
+  int rc = use_device(c);
+  if (rc) return rc;
+  const Plan p = resolve(c, M, N, K);
+  const KernelEntry& e = kKernels[p.kernel];
+  if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
+    return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: more split tiles than stream-K counters");
+  const auto* xb = reinterpret_cast<const __bf16*>(x);
+  const unsigned sblocks = (unsigned)cdiv(M, 4);
+  using StatsFn = void (*)(const __bf16*, int64_t, int, int, float, float*);
+  static constexpr StatsFn kStats[2][4] = {
+      {row_stats_kernel<kNormLayer, 2>, row_stats_kernel<kNormLayer, 4>, row_stats_kernel<kNormLayer, 8>,
+       row_stats_kernel<kNormLayer, 16>},
+      {row_stats_kernel<kNormRms, 2>, row_stats_kernel<kNormRms, 4>, row_stats_kernel<kNormRms, 8>,
+       row_stats_kernel<kNormRms, 16>}};
+  const int ch = K <= 1024 ? 0 : K <= 2048 ? 1 : K <= 4096 ? 2 : 3;  // register row of 2..16 x 512
+  hipLaunchKernelGGL(kStats[norm == SYS1HIP_NORM_LAYER ? 0 : 1][ch], dim3(sblocks), dim3(256), 0, c->stream,
+                     xb, ldx, (int)M, (int)K, eps, c->stats);
+  HIP_TRY(hipGetLastError());
+  GemmArgs a = {};
+  a.x = xb;
+  a.w = reinterpret_cast<const __bf16*>(w_folded);
+  a.y = reinterpret_cast<__bf16*>(y);
+  a.ws = c->ws;
+  a.counters = c->counters;
+  a.ldx = ldx, a.ldw = ldw, a.ldr = 0, a.ldy = ldy;
+  a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)nout;
+  a.dp_tiles = (int)std::min<int64_t>(p.dp, 1 << 30);
+  a.stats = c->stats;
+  a.colsum = colsum;
+  hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)p.grid), dim3(e.threads), 0, c->stream, a);
   HIP_TRY(hipGetLastError());
   return SYS1HIP_OK;
 }

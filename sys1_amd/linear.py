@@ -128,7 +128,7 @@ class Linear:
 
 def pack_gated_weight(weight: torch.Tensor, device: HipDevice | None = None) -> torch.Tensor:
     """[2I, K] (gate rows then up rows) -> the interleaved layout the gated
-    epilogue reads (groups of 32 gate rows followed by their 32 up rows)."""
+    epilogue reads (groups of 16 gate rows followed by their 16 up rows)."""
     dev = device or load_device(weight.device.index or 0)
     _check_operand(weight, "weight", dev)
     w = weight.contiguous()

@@ -48,6 +48,9 @@ def test_flag_values_match_header():
     for name in ("EINVAL", "EALIGN", "EDEVICE", "ERANGE"):
         m = re.search(rf"#define SYS1HIP_{name} \((-\d+)\)", text)
         assert int(m.group(1)) == getattr(_lib, name)
+    for name in ("LAYER", "RMS"):
+        m = re.search(rf"#define SYS1HIP_NORM_{name} (\d+)", text)
+        assert int(m.group(1)) == getattr(_lib, f"NORM_{name}")
 
 
 def _no_gpu():
@@ -145,6 +148,53 @@ def test_rope_qkv_rejects_bad_arguments(kwargs, code):
 
 def test_rope_qkv_empty_batch_is_a_noop():
     assert _rope(M=0, x=None, y=None, cos=None, sin=None, pos=None) == _lib.OK
+
+
+def _norm(ctx=_ctx, x=_P, ldx=64, w=_P, ldw=64, colsum=_P, norm=1, eps=1e-5, y=_P, ldy=64, M=4, N=64,
+          K=64, epi=0):
+    L = _lib.load()
+    return L.sys1hip_norm_linear_bf16(ctx, x, ldx, w, ldw, colsum, norm, eps, y, ldy, M, N, K, epi)
+
+
+@pytest.mark.parametrize("kwargs,code", [
+    (dict(ctx=None), _lib.EINVAL),
+    (dict(norm=3), _lib.EINVAL),                                   # unknown norm
+    (dict(norm=_lib.NORM_LAYER, epi=_lib.EPI_SWIGLU), _lib.EINVAL),  # pairs the reference has only
+    (dict(norm=_lib.NORM_RMS, epi=_lib.EPI_GEGLU), _lib.EINVAL),
+    (dict(epi=_lib.EPI_RESIDUAL), _lib.EINVAL),
+    (dict(eps=-1.0), _lib.EINVAL),
+    (dict(eps=float("nan")), _lib.EINVAL),
+    (dict(M=-1), _lib.EINVAL),
+    (dict(epi=_lib.EPI_GEGLU, N=80), _lib.EINVAL),
+    (dict(colsum=None), _lib.EINVAL),                              # LayerNorm needs colsum
+    (dict(x=None), _lib.EINVAL),
+    (dict(ldy=32), _lib.EINVAL),
+    (dict(K=60, ldx=64, ldw=64), _lib.EALIGN),
+    (dict(colsum=_P + 4), _lib.EALIGN),
+    (dict(M=(1 << 20) + 1), _lib.ERANGE),
+])
+def test_norm_linear_rejects_bad_arguments(kwargs, code):
+    rc = _norm(**kwargs)
+    assert rc == code, (kwargs, rc, _lib.load().sys1hip_last_error(None))
+
+
+def test_norm_linear_rms_needs_no_colsum_and_empty_is_noop():
+    assert _norm(M=0, x=None, y=None) == _lib.OK
+    # RMSNorm without colsum passes validation up to the (dummy) device step,
+    # so only the empty batch can be checked here without a GPU.
+    assert _norm(M=0, norm=_lib.NORM_RMS, colsum=None, x=None, y=None) == _lib.OK
+
+
+def test_fold_norm_rejects_bad_arguments():
+    L = _lib.load()
+    f = L.sys1hip_fold_norm_weight
+    assert f(None, _P, _P, 1, _P, _P, 64, 64) == _lib.EINVAL
+    assert f(_ctx, _P, _P, 0, _P, _P, 64, 64) == _lib.EINVAL        # unknown norm
+    assert f(_ctx, _P, _P, 1, _P, None, 64, 64) == _lib.EINVAL      # LayerNorm needs colsum
+    assert f(_ctx, _P, None, 2, _P, None, 64, 64) == _lib.EINVAL    # gamma
+    assert f(_ctx, _P, _P, 1, _P, _P, 0, 64) == _lib.EINVAL
+    assert f(_ctx, _P, _P, 1, _P, _P, 64, 12) == _lib.EALIGN
+    assert f(_ctx, _P, _P + 4, 1, _P, _P, 64, 64) == _lib.EALIGN
 
 
 def test_pack_rejects_bad_arguments():

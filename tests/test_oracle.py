@@ -133,6 +133,43 @@ def test_silu_and_swiglu_reference_generator(orc):
     np.testing.assert_allclose(s, g, rtol=1e-6, atol=1e-5)
 
 
+def test_rms_norm_against_torch_and_closed_form(orc):
+    """Qwen3.5 RMSNorm(1 + w) (src/archs/qwen35_text.rs:178-203) against
+    torch's rms_norm in float64 with weight 1 + w, and a constant row c,
+    whose output is c (1 + w) / sqrt(c^2 + eps)."""
+    torch = pytest.importorskip("torch")
+    x = orc.fill_normal((37, 512), 71) * 3.0 + 0.5
+    w = orc.fill_normal((512,), 72, 0.2)
+    expect = torch.nn.functional.rms_norm(torch.from_numpy(x).double(), (512,),
+                                          weight=1.0 + torch.from_numpy(w).double(), eps=1e-6).numpy()
+    np.testing.assert_allclose(orc.rms_norm(x, w, 1e-6), expect, rtol=2e-6, atol=2e-6)
+    c = np.full((1, 64), -2.5, np.float32)
+    w2 = np.linspace(-0.5, 0.5, 64).astype(np.float32)
+    np.testing.assert_allclose(orc.rms_norm(c, w2, 1e-6)[0], -2.5 * (1 + w2) / np.sqrt(6.25 + 1e-6),
+                               rtol=1e-6)
+
+
+def test_layer_norm_bf16_rounding_sequence(orc):
+    """ModernBERT's bf16 LayerNorm: normalised value cast to bf16, times the
+    weight, rounded (candle-nn LayerNorm on a bf16 input).  Pinned by its
+    invariants: every output is a bf16 value; with weight 1 it equals the
+    rounded f32 norm; it is invariant to a per-row shift and a positive
+    per-row scale of the input (up to the eps term); it is torch's float64
+    layer_norm within bf16 rounding."""
+    torch = pytest.importorskip("torch")
+    x = orc.round_bf16(orc.fill_normal((20, 768), 73) * 2.0 + 1.0)
+    g = orc.round_bf16(1.0 + orc.fill_normal((768,), 74, 0.1))
+    y = orc.layer_norm_bf16(x, g, 1e-5)
+    np.testing.assert_array_equal(y, orc.round_bf16(y))
+    np.testing.assert_array_equal(orc.layer_norm_bf16(x, np.ones(768, np.float32), 1e-5),
+                                  orc.round_bf16(orc.layer_norm(x, np.ones(768, np.float32), None, 1e-5)))
+    y2 = orc.layer_norm_bf16(x * 4.0 + 3.0, g, 1e-5)
+    assert np.abs(y2 - y).max() <= 4 * 2.0 ** -8 * np.abs(y).max()
+    t = torch.nn.functional.layer_norm(torch.from_numpy(x).double(), (768,),
+                                       weight=torch.from_numpy(g).double(), eps=1e-5).numpy()
+    assert np.abs(y - t).max() <= 2 * 2.0 ** -8 * np.abs(t).max()
+
+
 def test_layer_norm_against_torch(orc):
     torch = pytest.importorskip("torch")
     x = orc.fill_normal((13, 768), 4) * 3 + 1
