@@ -42,6 +42,7 @@ class Proj:
     src_off: int    # first input column
     dst: str        # output buffer name
     resid: str | None = None
+    norm: str | None = None  # pre-norm of the input ("layer" / "rms"), fused when the stack has norms
 
     @property
     def nout(self) -> int:
@@ -73,14 +74,20 @@ class StackConfig:
 
 
 def modernbert(hidden: int, intermediate: int, layers: int, name: str) -> StackConfig:
+    """Pre-norms: attn_norm before Wqkv in every layer but the first (whose
+    attn_norm weight is absent, so `Norm::load(..).ok()` is None and the
+    input passes through, src/archs/modernbert.rs:846-851,865-868), mlp_norm
+    before Wi (:884)."""
     H, I = hidden, intermediate
-    layer = [
-        Proj("Wqkv", H, 3 * H, _lib.EPI_NONE, "h", 0, "qkv"),
-        Proj("attn.Wo", H, H, _lib.EPI_RESIDUAL, "qkv", 2 * H, "h", resid="h"),
-        Proj("Wi+geglu", H, 2 * I, _lib.EPI_GEGLU, "h", 0, "act"),
-        Proj("mlp.Wo", I, H, _lib.EPI_RESIDUAL, "act", 0, "h", resid="h"),
-    ]
-    return StackConfig(name, H, [list(layer) for _ in range(layers)],
+
+    def layer(i: int) -> list[Proj]:
+        return [
+            Proj("Wqkv", H, 3 * H, _lib.EPI_NONE, "h", 0, "qkv", norm="layer" if i > 0 else None),
+            Proj("attn.Wo", H, H, _lib.EPI_RESIDUAL, "qkv", 2 * H, "h", resid="h"),
+            Proj("Wi+geglu", H, 2 * I, _lib.EPI_GEGLU, "h", 0, "act", norm="layer"),
+            Proj("mlp.Wo", I, H, _lib.EPI_RESIDUAL, "act", 0, "h", resid="h"),
+        ]
+    return StackConfig(name, H, [layer(i) for i in range(layers)],
                        f"ModernBERT H={H} I={I} x{layers}: Wqkv {H}->{3 * H}, Wo {H}->{H}, "
                        f"Wi {H}->2x{I} (GeGLU), Wo {I}->{H}")
 
@@ -96,18 +103,18 @@ def qwen35(hidden: int, layers: int, heads: int, kv_heads: int, head_dim: int,
     builds heads*hd; src/archs/qwen35_text.rs:281-285)."""
     H = hidden
     mlp = [
-        Proj("gate_up+swiglu", H, 2 * intermediate, _lib.EPI_SWIGLU, "h", 0, "act"),
+        Proj("gate_up+swiglu", H, 2 * intermediate, _lib.EPI_SWIGLU, "h", 0, "act", norm="rms"),
         Proj("down", intermediate, H, _lib.EPI_RESIDUAL, "act", 0, "h", resid="h"),
     ]
     dn_in = 2 * dn_qk + 2 * dn_v + 2 * dn_heads  # qkv | z | b | a
     deltanet = [
-        Proj("in_proj_qkvzba", H, dn_in, _lib.EPI_NONE, "h", 0, "mix"),
+        Proj("in_proj_qkvzba", H, dn_in, _lib.EPI_NONE, "h", 0, "mix", norm="rms"),
         Proj("out_proj", dn_v, H, _lib.EPI_RESIDUAL, "mix", 2 * dn_qk + dn_v, "h", resid="h"),
     ] + mlp
     q_w = 2 * heads * head_dim
     attn_in = q_w + 2 * kv_heads * head_dim
     attention = [
-        Proj("q_k_v", H, attn_in, _lib.EPI_NONE, "h", 0, "mix"),
+        Proj("q_k_v", H, attn_in, _lib.EPI_NONE, "h", 0, "mix", norm="rms"),
         Proj("o_proj", o_in, H, _lib.EPI_RESIDUAL, "mix", 0, "h", resid="h"),
     ] + mlp
     if layer_types is None:
@@ -131,12 +138,22 @@ CONFIGS = {
 }
 
 
+NORM_EPS = {"layer": 1e-5, "rms": 1e-6}  # ModernBERT layer_norm_eps, Qwen3.5 rms_norm_eps
+
+
 class ProjectionStack:
     """Weights and activation buffers of a stack on one GPU, and the layer
-    loop that enqueues its projections."""
+    loop that enqueues its projections.
+
+    norms=True fuses each projection's pre-norm (Proj.norm) into it
+    (sys1hip_norm_linear_bf16) with the norm weights of a fresh model --
+    LayerNorm weight 1, RMSNorm weight 0 (alpha 1) -- or `norm_weights`
+    [layer][projection] (f32 [K] or None).  norms=False runs the
+    projections alone."""
 
     def __init__(self, cfg: StackConfig, dev: HipDevice, max_tokens: int, seed: int = 0,
-                 weights: list[list[torch.Tensor]] | None = None, w_std: float = 0.02):
+                 weights: list[list[torch.Tensor]] | None = None, w_std: float = 0.02,
+                 norms: bool = False, norm_weights: list[list[torch.Tensor | None]] | None = None):
         self.cfg = cfg
         self.dev = dev
         self.max_tokens = max_tokens
@@ -144,9 +161,12 @@ class ProjectionStack:
         g = torch.Generator(device=d)
         g.manual_seed(seed)
         from .linear import pack_gated_weight
+        from .norm import fold_norm_weight
+        self.norms = norms
         self.weights: list[list[torch.Tensor]] = []
+        self.colsums: list[list[torch.Tensor | None]] = []
         for li, layer in enumerate(cfg.layers):
-            ws = []
+            ws, cs = [], []
             for pi, p in enumerate(layer):
                 if weights is not None:
                     w = weights[li][pi].to(device=d, dtype=torch.bfloat16).contiguous()
@@ -155,8 +175,16 @@ class ProjectionStack:
                          ).to(torch.bfloat16)
                 if p.epi in (_lib.EPI_GEGLU, _lib.EPI_SWIGLU):
                     w = pack_gated_weight(w, dev)
+                c = None
+                if norms and p.norm:
+                    gw = norm_weights[li][pi] if norm_weights is not None else None
+                    if gw is None:
+                        gw = torch.ones(p.K) if p.norm == "layer" else torch.zeros(p.K)
+                    w, c = fold_norm_weight(w, gw, p.norm, dev)
                 ws.append(w)
+                cs.append(c)
             self.weights.append(ws)
+            self.colsums.append(cs)
         widths: dict[str, int] = {"h": cfg.hidden}
         for layer in cfg.layers:
             for p in layer:
@@ -165,6 +193,7 @@ class ProjectionStack:
         self.buffers = {k: torch.zeros(max_tokens, (v + 7) // 8 * 8, dtype=torch.bfloat16, device=d)
                         for k, v in widths.items()}
         self._fn = dev._L.sys1hip_linear_bf16
+        self._norm_fn = dev._L.sys1hip_norm_linear_bf16
 
     def _calls(self, x: torch.Tensor, M: int) -> list[tuple]:
         """Argument tuples of every launch for M tokens (prepared once per M,
@@ -194,18 +223,29 @@ class ProjectionStack:
                     else:
                         rptr, ldr = bufs["h"].data_ptr(), bufs["h"].stride(0)
                 w = self.weights[li][pi]
-                calls.append((p, (src, ldx, w.data_ptr(), w.stride(0), None, rptr, ldr,
-                                  dst.data_ptr(), dst.stride(0), M, p.N, p.K, p.epi)))
+                if self.norms and p.norm:
+                    c = self.colsums[li][pi]
+                    calls.append((p, self._norm_fn, (
+                        src, ldx, w.data_ptr(), w.stride(0), c.data_ptr() if c is not None else None,
+                        _lib.NORM_LAYER if p.norm == "layer" else _lib.NORM_RMS, NORM_EPS[p.norm],
+                        dst.data_ptr(), dst.stride(0), M, p.N, p.K, p.epi)))
+                else:
+                    calls.append((p, self._fn, (src, ldx, w.data_ptr(), w.stride(0), None, rptr, ldr,
+                                                dst.data_ptr(), dst.stride(0), M, p.N, p.K, p.epi)))
         return calls
 
     def prepare(self, x: torch.Tensor, M: int):
+        """[(projection, C function, argument tuple)] of every launch."""
         ctx = self.dev.ctx
-        return [(p, (ctx, *[ctypes.c_void_p(a) if i in (0, 2, 4, 5, 7) and a is not None else a
-                            for i, a in enumerate(args)])) for p, args in self._calls(x, M)]
+        out = []
+        for p, fn, args in self._calls(x, M):
+            ptrs = (0, 2, 4, 7) if fn is self._norm_fn else (0, 2, 4, 5, 7)
+            out.append((p, fn, (ctx, *[ctypes.c_void_p(a) if i in ptrs and a is not None else a
+                                      for i, a in enumerate(args)])))
+        return out
 
     def run_prepared(self, prepared) -> None:
-        fn = self._fn
-        for _, args in prepared:
+        for _, fn, args in prepared:
             rc = fn(*args)
             if rc:
                 _lib.check(rc, self.dev.ctx)

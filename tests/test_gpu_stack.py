@@ -256,6 +256,76 @@ def test_projection_stack_matches_module_chain(dev, orc):
     assert torch.equal(out, h)
 
 
+def _oracle_chain_prenorm(orc, cfg, x, ws):
+    """The f32 chain with each projection's own pre-norm (Proj.norm): the
+    reference layer order, norm weights of a fresh model (LayerNorm weight
+    1, eps 1e-5; RMSNorm weight 0, eps 1e-6)."""
+    h = x.astype(np.float32)
+    mix = None
+    for li, layer in enumerate(cfg.layers):
+        for pi, p in enumerate(layer):
+            if p.src == "h":
+                src = h
+                if p.norm == "layer":
+                    src = orc.layer_norm(h, np.ones(h.shape[-1], np.float32), None, 1e-5)
+                elif p.norm == "rms":
+                    src = orc.rms_norm(h, np.zeros(h.shape[-1], np.float32), 1e-6)
+            else:
+                src = np.ascontiguousarray(mix[:, p.src_off:p.src_off + p.K])
+            out = _project_ref(orc, p, src, ws[li][pi], h if p.resid else None)
+            if p.dst == "h":
+                h = out
+            else:
+                mix = out
+    return h
+
+
+@pytest.mark.parametrize("family,M", [("modernbert", 1024), ("qwen", 512)])
+def test_stack_with_fused_norms_matches_f32_chain(dev, orc, family, M):
+    """The bench stack with its pre-norms fused (ProjectionStack(norms=True):
+    ModernBERT's LayerNorms before Wqkv (not in layer 0) and Wi, Qwen's
+    RMSNorms before in_proj / q,k,v and gate/up) against the f32 chain with
+    the same norms unfused."""
+    from sys1_amd.stacks import ProjectionStack, modernbert, qwen35
+    if family == "modernbert":
+        cfg = modernbert(768, 1152, 4, "modernbert-base-4")
+    else:
+        cfg = qwen35(2048, 4, 16, 2, 128, 6144, 2048, 4096, 16, 2048, "qwen35-small-4")
+    print(f"[gpu] {cfg.name} fused pre-norm stack M={M}", flush=True)
+    x = orc.fill_normal((M, cfg.hidden), 17)
+    ws = _weights(orc, cfg, 500)
+    stack = ProjectionStack(cfg, dev, M, weights=[[to_gpu_bf16(w, torch) for w in l] for l in ws],
+                            norms=True)
+    h_gpu = to_np(stack.forward(to_gpu_bf16(x, torch), M))
+    torch.cuda.synchronize()
+    h_ref = _oracle_chain_prenorm(orc, cfg, x, ws)
+    rel, mx = parity(h_gpu, h_ref)
+    print(f"[gpu] {cfg.name} final hidden vs f32 chain: rel_fro={rel:.3e} max={mx:.3e}", flush=True)
+    assert rel < CHAIN_TOL and mx < 5 * CHAIN_TOL
+
+
+def test_fused_norm_stack_matches_module_chain(dev, orc):
+    """The stack's pre-norm calls are the NormLinear module's calls: the
+    two chains agree bit for bit."""
+    from sys1_amd.linear import Linear
+    from sys1_amd.norm import NormLinear
+    from sys1_amd.stacks import ProjectionStack, modernbert
+    cfg = modernbert(768, 1152, 3, "modernbert-base-3")
+    M = 777
+    x = to_gpu_bf16(orc.fill_normal((M, 768), 5), torch)
+    ws = [[(torch.randn(p.N, p.K, device="cuda") * 0.02).to(torch.bfloat16) for p in layer]
+          for layer in cfg.layers]
+    out = ProjectionStack(cfg, dev, M, weights=ws, norms=True).forward(x, M).clone()
+    h = x
+    for li, (wqkv, wo, wi, wo2) in enumerate(ws):
+        qkv = (NormLinear(wqkv, torch.ones(768), "layer", 1e-5, device=dev) if li else
+               Linear(wqkv, device=dev))(h)
+        h = Linear(wo, device=dev)(qkv[:, 1536:], residual=h)
+        g = NormLinear(wi, torch.ones(768), "layer", 1e-5, "gelu", device=dev)(h)
+        h = Linear(wo2, device=dev)(g, residual=h)
+    assert torch.equal(out, h)
+
+
 @pytest.mark.parametrize("M,layers", [(64, 4), (256, 4), (1024, 4), (4096, 2), (16384, 1)])
 def test_modernbert_large_chain(dev, orc, M, layers):
     """BASELINE config 3 shapes (hidden 1024, GeGLU 2x2624) over its whole M
