@@ -148,12 +148,13 @@ class ProjectionStack:
     norms=True fuses each projection's pre-norm (Proj.norm) into it
     (sys1hip_norm_linear_bf16) with the norm weights of a fresh model --
     LayerNorm weight 1, RMSNorm weight 0 (alpha 1) -- or `norm_weights`
-    [layer][projection] (f32 [K] or None).  norms=False runs the
-    projections alone."""
+    [layer][projection] (f32 [K] or None), with eps per kind (NORM_EPS, or
+    `norm_eps`).  norms=False runs the projections alone."""
 
     def __init__(self, cfg: StackConfig, dev: HipDevice, max_tokens: int, seed: int = 0,
                  weights: list[list[torch.Tensor]] | None = None, w_std: float = 0.02,
-                 norms: bool = False, norm_weights: list[list[torch.Tensor | None]] | None = None):
+                 norms: bool = False, norm_weights: list[list[torch.Tensor | None]] | None = None,
+                 norm_eps: dict[str, float] | None = None):
         self.cfg = cfg
         self.dev = dev
         self.max_tokens = max_tokens
@@ -163,6 +164,7 @@ class ProjectionStack:
         from .linear import pack_gated_weight
         from .norm import fold_norm_weight
         self.norms = norms
+        self.norm_eps = dict(NORM_EPS, **(norm_eps or {}))
         self.weights: list[list[torch.Tensor]] = []
         self.colsums: list[list[torch.Tensor | None]] = []
         for li, layer in enumerate(cfg.layers):
@@ -227,7 +229,7 @@ class ProjectionStack:
                     c = self.colsums[li][pi]
                     calls.append((p, self._norm_fn, (
                         src, ldx, w.data_ptr(), w.stride(0), c.data_ptr() if c is not None else None,
-                        _lib.NORM_LAYER if p.norm == "layer" else _lib.NORM_RMS, NORM_EPS[p.norm],
+                        _lib.NORM_LAYER if p.norm == "layer" else _lib.NORM_RMS, self.norm_eps[p.norm],
                         dst.data_ptr(), dst.stride(0), M, p.N, p.K, p.epi)))
                 else:
                     calls.append((p, self._fn, (src, ldx, w.data_ptr(), w.stride(0), None, rptr, ldr,

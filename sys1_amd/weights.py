@@ -17,9 +17,17 @@ blocks the projection stacks fuse into one GEMM:
                 mlp.gate_proj|up_proj -> one (gate rows first), mlp.down_proj
               (src/archs/qwen35_text.rs:205-240,266-285,441-478,905-928)
 
-`read_projection_weights` is host-only (CPU tensors, shapes validated
-against the stack); `load_stack` puts them on the device as a
-ProjectionStack (gated weights pre-packed once there).
+Pre-norm weights (for a stack with its norms fused) by the same names:
+  ModernBERT  layers.{i}.attn_norm (before Wqkv; absent in layer 0),
+              layers.{i}.mlp_norm (before Wi)  (src/archs/modernbert.rs:846-852)
+  Qwen3.5     layers.{i}.input_layernorm (before in_proj / q,k,v),
+              layers.{i}.post_attention_layernorm (before gate/up)
+              (src/archs/qwen35_text.rs:916-927)
+
+`read_projection_weights` / `read_norm_weights` are host-only (CPU tensors,
+shapes validated against the stack); `load_stack` puts them on the device as
+a ProjectionStack (gated weights pre-packed and norm weights folded once
+there).
 """
 from __future__ import annotations
 
@@ -115,13 +123,55 @@ def read_projection_weights(paths: str | list[str], family: str, cfg: StackConfi
     return weights
 
 
+def read_norm_weights(paths: str | list[str], family: str, cfg: StackConfig,
+                      prefix: str | None = None) -> list[list[torch.Tensor | None]]:
+    """f32 [K] CPU tensors of the pre-norm of each projection with one
+    (Proj.norm), None elsewhere.  KeyError / ValueError as above."""
+    from safetensors import safe_open
+    if family not in ("modernbert", "qwen35"):
+        raise ValueError(f"unknown family {family!r}")
+    paths = [paths] if isinstance(paths, (str, os.PathLike)) else list(paths)
+    prefix = prefix if prefix is not None else (MODERNBERT_PREFIX if family == "modernbert"
+                                                else QWEN35_PREFIX)
+    where = _index(paths)
+    handles = {p: safe_open(p, framework="pt", device="cpu") for p in paths}
+    out = []
+    for i, layer in enumerate(cfg.layers):
+        row = []
+        for proj in layer:
+            if not proj.norm:
+                row.append(None)
+                continue
+            if family == "modernbert":
+                leaf = "attn_norm" if proj.name == "Wqkv" else "mlp_norm"
+            else:
+                leaf = "post_attention_layernorm" if proj.name.startswith("gate_up") else "input_layernorm"
+            n = f"{prefix}layers.{i}.{leaf}.weight"
+            if n not in where:
+                raise KeyError(f"checkpoint has no tensor {n}")
+            g = handles[where[n]].get_tensor(n).to(torch.float32)
+            if tuple(g.shape) != (proj.K,):
+                raise ValueError(f"{n}: shape {tuple(g.shape)}, expected [{proj.K}]")
+            row.append(g.contiguous())
+        out.append(row)
+    return out
+
+
 def load_stack(paths: str | list[str], family: str, config: dict | str, dev, max_tokens: int,
-               prefix: str | None = None):
-    """ProjectionStack on `dev` with a checkpoint's projection weights."""
+               prefix: str | None = None, norms: bool = False):
+    """ProjectionStack on `dev` with a checkpoint's projection weights (and,
+    with norms=True, its pre-norm weights fused, with the config's eps)."""
     from .stacks import ProjectionStack
     if isinstance(config, (str, os.PathLike)):
         with open(config) as f:
             config = json.load(f)
     cfg = modernbert_config(config) if family == "modernbert" else qwen35_config(config)
     weights = read_projection_weights(paths, family, cfg, prefix)
-    return ProjectionStack(cfg, dev, max_tokens, weights=weights)
+    nw, eps = None, None
+    if norms:
+        nw = read_norm_weights(paths, family, cfg, prefix)
+        c = config.get("text_config", config)
+        eps = ({"layer": float(c.get("layer_norm_eps", 1e-5))} if family == "modernbert"
+               else {"rms": float(c.get("rms_norm_eps", 1e-6))})
+    return ProjectionStack(cfg, dev, max_tokens, weights=weights, norms=norms, norm_weights=nw,
+                           norm_eps=eps)

@@ -413,3 +413,51 @@ def test_stack_from_safetensors_checkpoint(dev, orc, tmp_path):
     rel, _ = parity(to_np(out), h)
     print(f"[gpu] checkpoint stack vs f32 oracle: rel_fro={rel:.3e}", flush=True)
     assert rel < CHAIN_TOL
+
+
+def test_stack_with_norms_from_safetensors_checkpoint(dev, orc, tmp_path):
+    """load_stack(norms=True): projection and pre-norm weights by the
+    reference's names (attn_norm from layer 1, mlp_norm), eps from the
+    config; equals the stack built from the same tensors and follows the f32
+    chain with those norms."""
+    st = pytest.importorskip("safetensors.torch")
+    from sys1_amd import weights as W
+    from sys1_amd.stacks import ProjectionStack
+    cfg_json = {"hidden_size": 128, "intermediate_size": 192, "num_hidden_layers": 2,
+                "num_attention_heads": 2, "layer_norm_eps": 1e-5}
+    g = torch.Generator().manual_seed(9)
+    t = {}
+    for i in range(2):
+        p = f"model.layers.{i}."
+        t[p + "attn.Wqkv.weight"] = torch.randn(384, 128, generator=g) * 0.05
+        t[p + "attn.Wo.weight"] = torch.randn(128, 128, generator=g) * 0.05
+        t[p + "mlp.Wi.weight"] = torch.randn(384, 128, generator=g) * 0.05
+        t[p + "mlp.Wo.weight"] = torch.randn(128, 192, generator=g) * 0.05
+        t[p + "mlp_norm.weight"] = 1.0 + 0.1 * torch.randn(128, generator=g)
+        if i:
+            t[p + "attn_norm.weight"] = 1.0 + 0.1 * torch.randn(128, generator=g)
+    path = str(tmp_path / "mn.safetensors")
+    st.save_file(t, path)
+    M = 300
+    xf = orc.fill_normal((M, 128), 19)
+    x = to_gpu_bf16(xf, torch)
+    print(f"[gpu] checkpoint stack with norms M={M}", flush=True)
+    out = W.load_stack(path, "modernbert", cfg_json, dev, M, norms=True).forward(x, M).clone()
+    cfg = W.modernbert_config(cfg_json)
+    ws = W.read_projection_weights(path, "modernbert", cfg)
+    nw = W.read_norm_weights(path, "modernbert", cfg)
+    direct = ProjectionStack(cfg, dev, M, weights=[[w.cuda() for w in l] for l in ws], norms=True,
+                             norm_weights=nw).forward(x, M)
+    assert torch.equal(out, direct)
+    h = to_np(x)
+    for li, layer in enumerate(cfg.layers):
+        f = [to_np(w) for w in ws[li]]
+        g0 = nw[li][0].numpy() if nw[li][0] is not None else None
+        src = orc.layer_norm(h, g0, None, 1e-5) if g0 is not None else h
+        qkv = orc.linear_f32(src, f[0])
+        h = orc.linear_f32(np.ascontiguousarray(qkv[:, 256:]), f[1]) + h
+        act = orc.geglu(orc.linear_f32(orc.layer_norm(h, nw[li][2].numpy(), None, 1e-5), f[2]))
+        h = orc.linear_f32(act, f[3]) + h
+    rel, _ = parity(to_np(out), h)
+    print(f"[gpu] checkpoint stack with norms vs f32 oracle: rel_fro={rel:.3e}", flush=True)
+    assert rel < CHAIN_TOL

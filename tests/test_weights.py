@@ -33,6 +33,8 @@ def _modernbert_ckpt(tmp_path, shards=1):
         t[p + "mlp.Wi.weight"] = _t(g, 192, 64)
         t[p + "mlp.Wo.weight"] = _t(g, 64, 96)
         t[p + "mlp_norm.weight"] = _t(g, 64)
+        if i > 0:  # ModernBERT's layer 0 has no attn_norm
+            t[p + "attn_norm.weight"] = _t(g, 64)
     names = sorted(t)
     paths = []
     for s in range(shards):
@@ -83,6 +85,8 @@ def test_qwen35_concatenations_follow_layer_types(tmp_path):
     t[p1 + "self_attn.v_proj.weight"] = _t(g, 16, 64)
     t[p1 + "self_attn.o_proj.weight"] = _t(g, 64, 2 * 16)
     for p in (p0, p1):
+        t[p + "input_layernorm.weight"] = _t(g, 64)
+        t[p + "post_attention_layernorm.weight"] = _t(g, 64)
         t[p + "mlp.gate_proj.weight"] = _t(g, 96, 64)
         t[p + "mlp.up_proj.weight"] = _t(g, 96, 64)
         t[p + "mlp.down_proj.weight"] = _t(g, 64, 96)
@@ -101,3 +105,25 @@ def test_qwen35_concatenations_follow_layer_types(tmp_path):
     for i, p in enumerate((p0, p1)):
         assert torch.equal(ws[i][2], torch.cat([b(p + "mlp.gate_proj.weight"), b(p + "mlp.up_proj.weight")]))
         assert torch.equal(ws[i][3], b(p + "mlp.down_proj.weight"))
+    nw = W.read_norm_weights(path, "qwen35", cfg)
+    for i, p in enumerate((p0, p1)):
+        assert torch.equal(nw[i][0], t[p + "input_layernorm.weight"])
+        assert nw[i][1] is None and nw[i][3] is None
+        assert torch.equal(nw[i][2], t[p + "post_attention_layernorm.weight"])
+
+
+def test_modernbert_norm_weights(tmp_path):
+    t, paths = _modernbert_ckpt(tmp_path, shards=2)
+    cfg = W.modernbert_config(MB_CFG)
+    nw = W.read_norm_weights(paths, "modernbert", cfg)
+    assert nw[0][0] is None  # layer 0: no attn_norm, the input passes through
+    assert torch.equal(nw[1][0], t["model.layers.1.attn_norm.weight"])
+    for i in range(2):
+        assert torch.equal(nw[i][2], t[f"model.layers.{i}.mlp_norm.weight"])
+        assert nw[i][1] is None and nw[i][3] is None
+    bad = dict(t)
+    del bad["model.layers.1.attn_norm.weight"]
+    path = str(tmp_path / "nonorm.safetensors")
+    st.save_file(bad, path)
+    with pytest.raises(KeyError, match="attn_norm"):
+        W.read_norm_weights(path, "modernbert", cfg)
