@@ -185,6 +185,27 @@ SYS1HIP_API int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t l
                                          int32_t norm, float eps, uint16_t* y, int64_t ldy,
                                          int64_t M, int64_t N, int64_t K, int32_t epilogue);
 
+/* Qwen3.5 DeltaNet in_proj with its causal conv + SiLU fused: replaces
+ * `x.apply(&self.qkv)` followed by causal_conv_silu / cuda_conv_silu
+ * (src/archs/qwen35_text.rs:515-526,632-650; CUDA src/kernels/qwen35.cu:3-29),
+ * and with norm = SYS1HIP_NORM_RMS also the input RMSNorm before it (:933).
+ *   w [N, K]: the in_proj rows, qkv first (conv_ch rows), then z, b, a (or
+ *   just the qkv rows, N = conv_ch); folded by sys1hip_fold_norm_weight when
+ *   norm is set;
+ *   conv_w bf16 [conv_ch, 4]: the conv1d weight [conv_ch, 1, 4], taps
+ *   oldest first; conv_ch a multiple of 4;
+ *   positions int32 [M]: token m's position within its sequence (packed
+ *   ragged rows; taps before a sequence's first token read zeros, as the
+ *   reference's left zero padding does).
+ * y[:, :conv_ch] = bf16(silu(c)), c accumulated over the 4 taps in bf16 from
+ * bf16 products of the bf16-rounded projection (the reference's rounding),
+ * and y[:, conv_ch:N] is the rounded projection.  M up to 2^20 rows. */
+SYS1HIP_API int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx,
+                                              const uint16_t* w, int64_t ldw, int32_t norm, float eps,
+                                              const uint16_t* conv_w, int64_t conv_ch,
+                                              const int32_t* positions, uint16_t* y, int64_t ldy,
+                                              int64_t M, int64_t N, int64_t K);
+
 /* Tuning and test knob, no counterpart in the reference: force how many
  * tiles a stream-K kernel runs whole before its stream phase, for every
  * later call on this context (-1 = automatic; clamped to the tile count).

@@ -24,6 +24,8 @@
 
 #define ORC_EXPORT __attribute__((visibility("default")))
 
+ORC_EXPORT float orc_round_bf16(float v);
+
 /* ---------------------------------------------------------------- GEMM ---- */
 
 /* y[M,N] = x[M,K] . w[N,K]^T (+ bias[N]), f32 accumulation.
@@ -179,6 +181,34 @@ ORC_EXPORT void orc_rms_norm(const float* x, int64_t ldx, const float* w, float 
         const float scale = 1.0f / sqrtf(var + eps);
         for (int64_t h = 0; h < H; ++h) y[m * ldy + h] = x[m * ldx + h] * scale * (1.0f + w[h]);
     }
+}
+
+/* Qwen3.5 DeltaNet causal depthwise conv + SiLU over packed ragged rows
+ * (src/archs/qwen35_text.rs:632-650 causal_conv_silu; the CUDA kernel
+ * src/kernels/qwen35.cu:3-29 computes the same): for token m at position
+ * pos[m] of its sequence and channel c,
+ *   v = sum over tap = 0..kernel-1 of p[m + tap - kernel + 1, c] * w[c, tap],
+ * taps before the sequence start (pos[m] + tap - kernel + 1 < 0) reading the
+ * zero padding; out = v / (1 + e^-v).  bf16 != 0 applies the reference's bf16
+ * arithmetic: every product and every partial sum rounded to bf16, the
+ * result rounded once more after the SiLU. */
+ORC_EXPORT void orc_conv_silu(const float* p, int64_t ldp, const float* w, const int32_t* pos,
+                              int64_t M, int64_t C, int64_t kernel, int bf16, float* out,
+                              int64_t ldo) {
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t c = 0; c < C; ++c) {
+            float v = 0.0f;
+            for (int64_t tap = 0; tap < kernel; ++tap) {
+                const int64_t back = kernel - 1 - tap;
+                if (pos[m] < back) continue;
+                float prod = p[(m - back) * ldp + c] * w[c * kernel + tap];
+                if (bf16) prod = orc_round_bf16(prod);
+                v = v + prod;
+                if (bf16) v = orc_round_bf16(v);
+            }
+            float y = v / (1.0f + expf(-v));
+            out[m * ldo + c] = bf16 ? orc_round_bf16(y) : y;
+        }
 }
 
 /* Argmax with ties broken towards the lowest index (src/models/laya.rs:909-916:

@@ -47,6 +47,8 @@ def lib():
         L.orc_add_inplace.argtypes = [_f32p, _i64, _f32p, _i64, _i64, _i64]
         L.orc_layer_norm.argtypes = [_f32p, _i64, _f32p, _f32p, ctypes.c_float, _f32p, _i64, _i64, _i64]
         L.orc_rms_norm.argtypes = [_f32p, _i64, _f32p, ctypes.c_float, _f32p, _i64, _i64, _i64]
+        L.orc_conv_silu.argtypes = [_f32p, _i64, _f32p, ctypes.POINTER(ctypes.c_int32), _i64, _i64, _i64,
+                                    ctypes.c_int, _f32p, _i64]
         L.orc_argmax.argtypes = [_f32p, _i64]
         L.orc_argmax.restype = _i64
         L.orc_round_bf16.argtypes = [ctypes.c_float]
@@ -183,6 +185,23 @@ def rms_norm(x, weight, eps=1e-6) -> np.ndarray:
     w = _f32(weight)
     lib().orc_rms_norm(_p(x2), H, _p(w), eps, _p(y), H, x2.shape[0], H)
     return y.reshape(x.shape)
+
+
+def conv_silu(projected, weight, positions, bf16=True) -> np.ndarray:
+    """Qwen3.5 DeltaNet causal conv + SiLU over packed rows
+    (src/archs/qwen35_text.rs:632-650): projected [M, C], weight [C, k]
+    (the conv1d weight [C, 1, k] squeezed), positions [M] (each token's
+    position within its sequence).  bf16=True follows the reference's bf16
+    arithmetic (rounded products and partial sums)."""
+    p = _f32(projected)
+    w = _f32(weight)
+    M, C = p.shape
+    k = w.shape[1]
+    pos = np.ascontiguousarray(positions, np.int32)
+    out = np.empty((M, C), np.float32)
+    lib().orc_conv_silu(_p(p), C, _p(w), pos.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)), M, C, k,
+                        1 if bf16 else 0, _p(out), C)
+    return out
 
 
 def argmax(v) -> int:

@@ -37,7 +37,7 @@ EXPORTS = (
     "sys1hip_pack_gated_weight", "sys1hip_query_kernel", "sys1hip_set_kernel",
     "sys1hip_kernel_count", "sys1hip_kernel_name", "sys1hip_set_grid",
     "sys1hip_set_dp_tiles", "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
-    "sys1hip_norm_linear_bf16",
+    "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16",
 )
 
 
@@ -80,6 +80,8 @@ def load() -> ctypes.CDLL:
     L.sys1hip_fold_norm_weight.argtypes = [vp, vp, vp, i32, vp, vp, i64, i64]
     L.sys1hip_norm_linear_bf16.argtypes = [vp, vp, i64, vp, i64, vp, i32, ctypes.c_float, vp, i64,
                                            i64, i64, i64, i32]
+    L.sys1hip_linear_conv_silu_bf16.argtypes = [vp, vp, i64, vp, i64, i32, ctypes.c_float, vp, i64, vp,
+                                                vp, i64, i64, i64, i64]
     L.sys1hip_kernel_count.argtypes = []
     L.sys1hip_kernel_name.argtypes = [i32]
     L.sys1hip_kernel_name.restype = ctypes.c_char_p
@@ -87,7 +89,7 @@ def load() -> ctypes.CDLL:
                  "sys1hip_linear_bf16", "sys1hip_pack_gated_weight", "sys1hip_query_kernel",
                  "sys1hip_set_kernel", "sys1hip_set_grid", "sys1hip_set_dp_tiles",
                  "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
-                 "sys1hip_norm_linear_bf16", "sys1hip_kernel_count"):
+                 "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_kernel_count"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

@@ -35,21 +35,29 @@ enum Epi : int {
   kEpiNormLnGeglu = 9,
   kEpiNormRms = 10,
   kEpiNormRmsSwiglu = 11,
-  kEpiCount = 12,
+  // Qwen3.5 DeltaNet in_proj: causal conv (4 taps) + SiLU over the first
+  // conv_ch columns, the rest plain; optionally after an RMSNorm.
+  kEpiConvSilu = 12,
+  kEpiNormRmsConvSilu = 13,
+  kEpiCount = 14,
 };
+
+constexpr int kConvTaps = 4;  // DeltaNet conv kernel size (linear_conv_kernel_dim)
+constexpr int kConvHalo = kConvTaps - 1;
 
 enum NormKind : int { kNormNone = 0, kNormLayer = 1, kNormRms = 2 };
 
 __host__ __device__ constexpr int epi_norm(int e) {
-  return e == kEpiNormLn || e == kEpiNormLnGeglu ? kNormLayer
-         : e == kEpiNormRms || e == kEpiNormRmsSwiglu ? kNormRms
-                                                      : kNormNone;
+  return e == kEpiNormLn || e == kEpiNormLnGeglu                              ? kNormLayer
+         : e == kEpiNormRms || e == kEpiNormRmsSwiglu || e == kEpiNormRmsConvSilu ? kNormRms
+                                                                                   : kNormNone;
 }
 // The epilogue applied after the normalisation.
 __host__ __device__ constexpr int epi_base(int e) {
   return e == kEpiNormLn || e == kEpiNormRms ? kEpiNone
          : e == kEpiNormLnGeglu              ? kEpiGeglu
          : e == kEpiNormRmsSwiglu            ? kEpiSwiglu
+         : e == kEpiNormRmsConvSilu          ? kEpiConvSilu
                                              : e;
 }
 __host__ __device__ constexpr bool epi_gated(int e) {
@@ -146,6 +154,10 @@ struct GemmArgs {
   // 1/sqrt(var + eps) of input row m; colsum[n] = sum_k w[n, k] (LayerNorm).
   const float* stats;
   const float* colsum;
+  // Conv epilogues: conv_w bf16 [conv_ch, 4] (taps oldest first), pos[m] =
+  // token m's position in its sequence.
+  const __bf16* conv_w;
+  int conv_ch;
 };
 
 // Map the hardware workgroup id to a logical tile id so that each XCD gets a

@@ -156,6 +156,7 @@ struct Segment {
 // over every CU.
 struct TileWalk {
   int tiles_m, tiles_n, kt_count, tiles, dp_tiles;
+  int step_m;  // rows between tile rows: BM, or BM - halo (tile rows overlap by the halo)
   // tile phase
   int first, count, stride;
   // stream phase
@@ -165,8 +166,11 @@ struct TileWalk {
 
   static constexpr int kGroupM = 4;
 
-  __device__ TileWalk(int M, int N, int K, int BM, int BN, int BK, int dp) {
-    tiles_m = (M + BM - 1) / BM;
+  // halo > 0: tile row tm covers rows [tm (BM - halo), + BM), so the halo
+  // rows before each tile row's outputs are computed in the same tile.
+  __device__ TileWalk(int M, int N, int K, int BM, int BN, int BK, int dp, int halo = 0) {
+    step_m = BM - halo;
+    tiles_m = M <= BM ? 1 : 1 + (M - BM + step_m - 1) / step_m;
     tiles_n = (N + BN - 1) / BN;
     kt_count = (K + BK - 1) / BK;
     tiles = tiles_m * tiles_n;
@@ -193,6 +197,7 @@ struct TileWalk {
     end = (int)blockIdx.x < sgrid ? start(blockIdx.x + 1) : 0;
   }
   __device__ int start(int g) const { return (int)((int64_t)g * total / sgrid); }
+  __device__ int row0(int tm) const { return tm * step_m; }
 
   // Tile index -> coordinates (grouped raster).
   __device__ void tile_coords(int t, int& tm, int& tn) const {
@@ -254,7 +259,9 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
   constexpr int BK = S::BK;
   __shared__ __attribute__((aligned(1024))) char lds[S::kLdsBytes];
 
-  const TileWalk walk(a.M, a.N, a.K, BM, BN, BK, STREAMK ? a.dp_tiles : 1 << 30);
+  constexpr bool kConv = epi_base(EPI) == kEpiConvSilu;
+  static_assert(!kConv || WM == 1, "conv epilogue: one wave row per tile");
+  const TileWalk walk(a.M, a.N, a.K, BM, BN, BK, STREAMK ? a.dp_tiles : 1 << 30, kConv ? kConvHalo : 0);
   if (walk.steps() == 0) return;
 
   const int tid = threadIdx.x;
@@ -284,7 +291,7 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
   };
   unsigned src_off[S::kDma];
   auto set_offsets = [&](const Segment& sg) {
-    const int x_left = a.M - 1 - sg.tm * BM, w_left = a.N - 1 - sg.tn * BN;
+    const int x_left = a.M - 1 - walk.row0(sg.tm), w_left = a.N - 1 - sg.tn * BN;
 #pragma unroll
     for (int i = 0; i < S::kDma; ++i) {
       const int r = dma_row(i);
@@ -310,7 +317,7 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
   };
   auto refill_at = [&](int stage, bool live) {
     Refill r;
-    const int m0 = isg.tm * BM, n0 = isg.tn * BN;
+    const int m0 = walk.row0(isg.tm), n0 = isg.tn * BN;
     const int bytes = live ? 0x7ffffff0 : 0;
     r.base = lds + stage * S::kStageBytes;
     r.xr = make_rsrc_uniform(reinterpret_cast<const char*>(a.x + (int64_t)m0 * a.ldx) + is_kt * BK * 2, bytes);
@@ -467,8 +474,131 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
             else acc[i][j][4 * g + e] = v * rs[j];
           }
   };
-  auto epilogue = [&](int m0, int n0) {
+  // DeltaNet causal conv + SiLU over the in_proj qkv columns
+  // (src/archs/qwen35_text.rs:515-526,632-650; src/kernels/qwen35.cu:3-29):
+  // out[r, n] = silu(sum over taps t = 3..0 of w[n, 3 - t] * p[r - t, n]),
+  // p = the bf16-rounded projection, each product rounded to bf16 and added
+  // in bf16, taps before the row's sequence start (pos[r] < t) skipped;
+  // columns from conv_ch on are the plain projection (z, b, a).  The wave
+  // holds all rows of the tile (WM = 1): row R = 32 j + lane % 32 of block
+  // j, so row R - t is lane - t of block j, or lane + 32 - t of block j - 1.
+  // One ds_bpermute per tap moves a bf16 pair: each lane offers block j's
+  // value, or block j - 1's when it is among the last t lanes of its half.
+  // Rows below `skip` are the tile's halo (computed, not stored).
+  auto conv_epilogue = [&](int m0, int n0, int skip) {
+    const int h = fk;
+    int pos[S::FM];
+#pragma unroll
+    for (int j = 0; j < S::FM; ++j) {
+      const int m = m0 + j * 32 + frow;
+      pos[j] = m < a.M ? a.pos[m] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < S::FN; ++i) {
+      bf16x4 o[S::FM][4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + wn * S::TN + i * 32 + 8 * g + 4 * h;  // features n .. n+3 (conv_ch % 4 == 0)
+        float p[S::FM][4];
+#pragma unroll
+        for (int j = 0; j < S::FM; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) p[j][e] = round_bf16(acc[i][j][4 * g + e]);
+        if (n < a.conv_ch) {
+          // taps of features n .. n+3: 16 bf16, row-major [feature][tap]
+          const bf16x8 w01 = *reinterpret_cast<const bf16x8*>(a.conv_w + (int64_t)n * kConvTaps);
+          const bf16x8 w23 = *reinterpret_cast<const bf16x8*>(a.conv_w + (int64_t)n * kConvTaps + 8);
+          float cw[4][kConvTaps];
+#pragma unroll
+          for (int q = 0; q < kConvTaps; ++q) {
+            cw[0][q] = to_f32(w01[q]);
+            cw[1][q] = to_f32(w01[4 + q]);
+            cw[2][q] = to_f32(w23[q]);
+            cw[3][q] = to_f32(w23[4 + q]);
+          }
+          // packed bf16 pairs of each block: (e0, e1), (e2, e3)
+          unsigned pk[S::FM][2];
+#pragma unroll
+          for (int j = 0; j < S::FM; ++j)
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              bf16x4 b4;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) b4[e] = to_bf16(p[j][e]);
+              pk[j][u] = __builtin_bit_cast(i32x2, b4)[u];
+            }
+          float val[S::FM][4];
+#pragma unroll
+          for (int j = 0; j < S::FM; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) val[j][e] = 0.0f;
+#pragma unroll
+          for (int t = kConvTaps - 1; t >= 0; --t) {  // oldest tap first, as the reference adds them
+            float x[S::FM][4];
+            if (t == 0) {
+#pragma unroll
+              for (int j = 0; j < S::FM; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[j][e] = p[j][e];
+            } else {
+              const int src = (lane & 32) | (((lane & 31) - t) & 31);
+              const bool late = (lane & 31) >= 32 - t;  // offers the previous block's row
+#pragma unroll
+              for (int j = 0; j < S::FM; ++j)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                  const unsigned prev = j > 0 ? pk[j > 0 ? j - 1 : 0][u] : 0u;
+                  const unsigned offer = late ? prev : pk[j][u];
+                  const unsigned got = (unsigned)__shfl((int)offer, src, 64);
+                  const i32x2 g2 = {(int)(u == 0 ? got : 0), (int)(u == 1 ? got : 0)};
+                  const bf16x4 b4 = __builtin_bit_cast(bf16x4, g2);
+                  x[j][2 * u] = to_f32(b4[2 * u]);
+                  x[j][2 * u + 1] = to_f32(b4[2 * u + 1]);
+                }
+            }
+            const int tap = kConvTaps - 1 - t;
+#pragma unroll
+            for (int j = 0; j < S::FM; ++j)
+              if (pos[j] >= t) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  val[j][e] = round_bf16(val[j][e] + round_bf16(x[j][e] * cw[e][tap]));
+              }
+          }
+#pragma unroll
+          for (int j = 0; j < S::FM; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float v = val[j][e];
+              o[j][g][e] = to_bf16(v / (1.0f + expf(-v)));
+            }
+        } else {
+#pragma unroll
+          for (int j = 0; j < S::FM; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[j][g][e] = to_bf16(p[j][e]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < S::FM; ++j) {
+        const int r = j * 32 + frow;
+        const int m = m0 + r;
+        const bool row_ok = m < a.M && r >= skip;
+#pragma unroll
+        for (int gp = 0; gp < 2; ++gp) {
+          const bf16x8 v = pair16(o[j][2 * gp], o[j][2 * gp + 1]);
+          const int n = n0 + wn * S::TN + i * 32 + 16 * gp + 8 * h;
+          if (row_ok && n < a.Nout) store8(a.y + (int64_t)m * a.ldy + n, v, a.Nout - n);
+        }
+      }
+    }
+  };
+  auto epilogue = [&](int m0, int n0, int skip) {
     if constexpr (NORM != kNormNone) normalize_tile(m0, n0);
+    if constexpr (kConv) {
+      conv_epilogue(m0, n0, skip);
+      return;
+    }
     const int h = fk;
     const int out_n0 = epi_gated(E) ? (n0 + wn * S::TN) / 2 : n0 + wn * S::TN;
 #pragma unroll
@@ -769,9 +899,10 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
     __builtin_amdgcn_sched_barrier(0);
     if (++ckt == csg.kt1) {
       if constexpr (STREAMK) {
-        if (walk.complete(csg) || finish_partial(csg)) epilogue(csg.tm * BM, csg.tn * BN);
+        if (walk.complete(csg) || finish_partial(csg))
+          epilogue(walk.row0(csg.tm), csg.tn * BN, csg.tm ? kConvHalo : 0);
       } else {
-        epilogue(csg.tm * BM, csg.tn * BN);
+        epilogue(walk.row0(csg.tm), csg.tn * BN, csg.tm ? kConvHalo : 0);
       }
       zero_acc();
       if (s + 1 < steps) {

@@ -67,12 +67,20 @@ struct KernelEntry {
   int bk;               // k-tile depth
   int stages;           // LDS pipeline stages (stages - 1 k-tiles in flight)
   int tn;               // output columns per wave (the RoPE epilogue needs 64: one head)
+  int wm;               // waves along M (the conv epilogue needs 1: a wave holds every row)
   KernelFn fn[kEpiCount];
 };
 
+// The conv epilogues exist for shapes whose waves hold every row of a tile.
+template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK, int EPI>
+constexpr KernelFn conv_fn() {
+  if constexpr (WM == 1) return gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, EPI>;
+  else return nullptr;
+}
+
 template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK>
 constexpr KernelEntry tile_entry(const char* name, float eff) {
-  return KernelEntry{name, BM, BN, WM * WN * 64, OCC, SK, eff, BK, ST, BN / WN,
+  return KernelEntry{name, BM, BN, WM * WN * 64, OCC, SK, eff, BK, ST, BN / WN, WM,
                      {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 0>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 1>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 2>,
@@ -84,7 +92,9 @@ constexpr KernelEntry tile_entry(const char* name, float eff) {
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 8>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 9>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 10>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 11>}};
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 11>,
+                      conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 12>(),
+                      conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 13>()}};
 }
 
 // Output-tile shapes.  The first group serves large M (MFMA-bound); the
@@ -101,6 +111,10 @@ const KernelEntry kKernels[] = {
     tile_entry<128, 128, 2, 2, 4, 64, 1, true>("stream_128x128_s4_w2x2", 0.80f),
     tile_entry<128, 256, 2, 4, 3, 64, 1, true>("stream_128x256_s3_w2x4", 0.80f),
     tile_entry<256, 128, 4, 2, 3, 64, 1, true>("stream_256x128_s3_w4x2", 0.80f),
+    // Waves span every row of the tile (WM = 1): the shapes of the DeltaNet
+    // in_proj with its causal conv fused (the conv reads earlier rows).
+    tile_entry<128, 256, 1, 4, 2, 64, 1, false>("tile_128x256_s2_w1x4", 0.30f),
+    tile_entry<128, 256, 1, 4, 3, 64, 1, true>("stream_128x256_s3_w1x4", 0.30f),
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
@@ -212,12 +226,23 @@ void consider(const Context* c, int id, int64_t M, int64_t N, int64_t K, int64_t
 // tiles cannot fill the CUs, tile shapes above 128 tokens), or over the
 // forced kernel, grid and/or dp.  Stream-K grids from a quarter of
 // the slots up to all of them are tried.
-Plan resolve(const Context* c, int64_t M, int64_t N, int64_t K, bool head64 = false) {
+// Rows a kernel computes for M outputs when its tile rows overlap by `halo`
+// (the conv epilogue): whole tile rows, as the tile schedule counts them.
+int64_t halo_rows(const KernelEntry& e, int64_t M, int halo) {
+  if (halo == 0 || M <= e.bm) return M;
+  return (1 + cdiv(M - e.bm, e.bm - halo)) * e.bm;
+}
+
+// conv: only shapes with a conv epilogue (waves spanning every row), priced
+// on the rows their overlapping tile rows compute.
+Plan resolve(const Context* c, int64_t M0, int64_t N, int64_t K, bool head64 = false, bool conv = false) {
   Plan best;
   for (int id = 0; id < kNumKernels; ++id) {
     if (c->forced_kernel >= 0 && id != c->forced_kernel) continue;
     const KernelEntry& e = kKernels[id];
     if (head64 && e.tn != 64) continue;
+    if (conv && e.wm != 1) continue;
+    const int64_t M = conv ? halo_rows(e, M0, kConvHalo) : M0;
     if (c->forced_kernel < 0) {
       // Measured in the projection chains: the large-M hybrid loses to the
       // plain tile schedule (every split tile moves two f32 partials across
@@ -502,6 +527,28 @@ int sys1hip_linear_rope_qkv_bf16(void* ctx, const uint16_t* x, int64_t ldx, cons
   return SYS1HIP_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// Per-row (mean, 1/std) of x into the context's statistics buffer.
+int launch_row_stats(Context* c, const __bf16* x, int64_t ldx, int64_t M, int64_t K, int32_t norm,
+                     float eps) {
+  using StatsFn = void (*)(const __bf16*, int64_t, int, int, float, float*);
+  static constexpr StatsFn kStats[2][4] = {
+      {row_stats_kernel<kNormLayer, 2>, row_stats_kernel<kNormLayer, 4>, row_stats_kernel<kNormLayer, 8>,
+       row_stats_kernel<kNormLayer, 16>},
+      {row_stats_kernel<kNormRms, 2>, row_stats_kernel<kNormRms, 4>, row_stats_kernel<kNormRms, 8>,
+       row_stats_kernel<kNormRms, 16>}};
+  const int ch = K <= 1024 ? 0 : K <= 2048 ? 1 : K <= 4096 ? 2 : 3;  // register row of 2..16 x 512
+  hipLaunchKernelGGL(kStats[norm == SYS1HIP_NORM_LAYER ? 0 : 1][ch], dim3((unsigned)cdiv(M, 4)), dim3(256), 0,
+                     c->stream, x, ldx, (int)M, (int)K, eps, c->stats);
+  HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+}  // namespace
+
+extern "C" {
+
 int sys1hip_fold_norm_weight(void* ctx, const uint16_t* w, const float* gamma, int32_t norm,
                              uint16_t* w_folded, float* colsum, int64_t N, int64_t K) {
   if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_fold_norm_weight: null context");
@@ -575,17 +622,8 @@ int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const ui
   if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
     return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: more split tiles than stream-K counters");
   const auto* xb = reinterpret_cast<const __bf16*>(x);
-  const unsigned sblocks = (unsigned)cdiv(M, 4);
-  using StatsFn = void (*)(const __bf16*, int64_t, int, int, float, float*);
-  static constexpr StatsFn kStats[2][4] = {
-      {row_stats_kernel<kNormLayer, 2>, row_stats_kernel<kNormLayer, 4>, row_stats_kernel<kNormLayer, 8>,
-       row_stats_kernel<kNormLayer, 16>},
-      {row_stats_kernel<kNormRms, 2>, row_stats_kernel<kNormRms, 4>, row_stats_kernel<kNormRms, 8>,
-       row_stats_kernel<kNormRms, 16>}};
-  const int ch = K <= 1024 ? 0 : K <= 2048 ? 1 : K <= 4096 ? 2 : 3;  // register row of 2..16 x 512
-  hipLaunchKernelGGL(kStats[norm == SYS1HIP_NORM_LAYER ? 0 : 1][ch], dim3(sblocks), dim3(256), 0, c->stream,
-                     xb, ldx, (int)M, (int)K, eps, c->stats);
-  HIP_TRY(hipGetLastError());
+  rc = launch_row_stats(c, xb, ldx, M, K, norm, eps);
+  if (rc) return rc;
   GemmArgs a = {};
   a.x = xb;
   a.w = reinterpret_cast<const __bf16*>(w_folded);
@@ -597,6 +635,66 @@ int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const ui
   a.dp_tiles = (int)std::min<int64_t>(p.dp, 1 << 30);
   a.stats = c->stats;
   a.colsum = colsum;
+  hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)p.grid), dim3(e.threads), 0, c->stream, a);
+  HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+
+int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t ldw,
+                                  int32_t norm, float eps, const uint16_t* conv_w, int64_t conv_ch,
+                                  const int32_t* positions, uint16_t* y, int64_t ldy, int64_t M, int64_t N,
+                                  int64_t K) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: null context");
+  Context* c = static_cast<Context*>(ctx);
+  if (norm != 0 && norm != SYS1HIP_NORM_RMS)
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: norm %d (0 or SYS1HIP_NORM_RMS)", norm);
+  if (M < 0 || N <= 0 || K <= 0 || conv_ch <= 0 || conv_ch > N || conv_ch % 4 || !(eps >= 0.0f))
+    return fail(SYS1HIP_EINVAL,
+                "sys1hip_linear_conv_silu_bf16: bad shape M=%lld N=%lld K=%lld conv_ch=%lld (multiple of 4, "
+                "at most N) or eps",
+                (long long)M, (long long)N, (long long)K, (long long)conv_ch);
+  if (M == 0) return SYS1HIP_OK;
+  if (!x || !w || !y || !conv_w || !positions)
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: null pointer");
+  if (ldx < K || ldw < K || ldy < N)
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: leading dimension too small");
+  if (K % 8 || ldx % 8 || ldw % 8)
+    return fail(SYS1HIP_EALIGN, "sys1hip_linear_conv_silu_bf16: K, ldx and ldw must be multiples of 8");
+  if (!aligned16(x) || !aligned16(w) || !aligned16(conv_w))
+    return fail(SYS1HIP_EALIGN, "sys1hip_linear_conv_silu_bf16: x, w and conv_w must be 16-byte aligned");
+  if (M > kNormRows)
+    return fail(SYS1HIP_ERANGE, "sys1hip_linear_conv_silu_bf16: M=%lld above the %lld rows of one call",
+                (long long)M, (long long)kNormRows);
+  if (N > (1ll << 30) || K > (1ll << 30))
+    return fail(SYS1HIP_ERANGE, "sys1hip_linear_conv_silu_bf16: dimension above 2^30");
+  int rc = use_device(c);
+  if (rc) return rc;
+  const int epi = norm ? kEpiNormRmsConvSilu : kEpiConvSilu;
+  const Plan p = resolve(c, M, N, K, false, true);
+  const KernelEntry& e = kKernels[p.kernel];
+  if (!e.fn[epi])
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: kernel %s has no conv epilogue", e.name);
+  const int64_t rows = halo_rows(e, M, kConvHalo);
+  if (e.streamk && (cdiv(rows, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
+    return fail(SYS1HIP_ERANGE, "sys1hip_linear_conv_silu_bf16: more split tiles than stream-K counters");
+  const auto* xb = reinterpret_cast<const __bf16*>(x);
+  if (norm) {
+    rc = launch_row_stats(c, xb, ldx, M, K, norm, eps);
+    if (rc) return rc;
+  }
+  GemmArgs a = {};
+  a.x = xb;
+  a.w = reinterpret_cast<const __bf16*>(w);
+  a.y = reinterpret_cast<__bf16*>(y);
+  a.ws = c->ws;
+  a.counters = c->counters;
+  a.ldx = ldx, a.ldw = ldw, a.ldr = 0, a.ldy = ldy;
+  a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)N;
+  a.dp_tiles = (int)std::min<int64_t>(p.dp, 1 << 30);
+  a.stats = c->stats;
+  a.pos = positions;
+  a.conv_w = reinterpret_cast<const __bf16*>(conv_w);
+  a.conv_ch = (int)conv_ch;
   hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)p.grid), dim3(e.threads), 0, c->stream, a);
   HIP_TRY(hipGetLastError());
   return SYS1HIP_OK;

@@ -197,6 +197,35 @@ def test_fold_norm_rejects_bad_arguments():
     assert f(_ctx, _P, _P + 4, 1, _P, _P, 64, 64) == _lib.EALIGN
 
 
+def _conv(ctx=_ctx, x=_P, ldx=64, w=_P, ldw=64, norm=0, eps=1e-6, cw=_P, C=64, pos=_P, y=_P, ldy=128,
+          M=4, N=128, K=64):
+    L = _lib.load()
+    return L.sys1hip_linear_conv_silu_bf16(ctx, x, ldx, w, ldw, norm, eps, cw, C, pos, y, ldy, M, N, K)
+
+
+@pytest.mark.parametrize("kwargs,code", [
+    (dict(ctx=None), _lib.EINVAL),
+    (dict(norm=_lib.NORM_LAYER), _lib.EINVAL),     # RMSNorm only (Qwen3.5)
+    (dict(C=0), _lib.EINVAL),
+    (dict(C=130), _lib.EINVAL),                    # more conv channels than N
+    (dict(C=62), _lib.EINVAL),                     # multiple of 4
+    (dict(M=-1), _lib.EINVAL),
+    (dict(pos=None), _lib.EINVAL),
+    (dict(cw=None), _lib.EINVAL),
+    (dict(ldy=64), _lib.EINVAL),
+    (dict(K=60, ldx=64, ldw=64), _lib.EALIGN),
+    (dict(cw=_P + 8), _lib.EALIGN),
+    (dict(M=(1 << 20) + 1), _lib.ERANGE),
+])
+def test_conv_rejects_bad_arguments(kwargs, code):
+    rc = _conv(**kwargs)
+    assert rc == code, (kwargs, rc, _lib.load().sys1hip_last_error(None))
+
+
+def test_conv_empty_batch_is_a_noop():
+    assert _conv(M=0, x=None, y=None, pos=None, cw=None) == _lib.OK
+
+
 def test_pack_rejects_bad_arguments():
     L = _lib.load()
     f = L.sys1hip_pack_gated_weight

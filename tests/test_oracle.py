@@ -170,6 +170,82 @@ def test_layer_norm_bf16_rounding_sequence(orc):
     assert np.abs(y - t).max() <= 2 * 2.0 ** -8 * np.abs(t).max()
 
 
+def _conv_ref_gen():
+    """The reference's own conv test inputs (src/archs/qwen35_text.rs:1266-1284):
+    batch 2, length 7, channels 31, kernel 4."""
+    b, L, C, k = 2, 7, 31, 4
+    p = (((np.arange(b * L * C) * 17) % 41) - 20).astype(np.float32) * 0.04
+    w = (((np.arange(C * k) * 11) % 23) - 11).astype(np.float32) * 0.02
+    return p.reshape(b * L, C), w.reshape(C, k), np.tile(np.arange(L, dtype=np.int32), b), (b, L, C, k)
+
+
+def test_conv_silu_f32_against_padded_loop_and_torch(orc):
+    """DeltaNet causal conv + SiLU (src/archs/qwen35_text.rs:632-650), f32:
+    a float64 restatement of the reference's padded-rectangle form
+    (pad_with_zeros, then tap-by-tap accumulation), and torch's depthwise
+    conv1d with left padding, on the reference's own test generator."""
+    torch = pytest.importorskip("torch")
+    p, w, pos, (b, L, C, k) = _conv_ref_gen()
+    got = orc.conv_silu(p, w, pos, bf16=False)
+    pr = p.reshape(b, L, C).astype(np.float64)
+    padded = np.concatenate([np.zeros((b, k - 1, C)), pr], axis=1)
+    mixed = np.zeros((b, L, C))
+    for tap in range(k):
+        mixed += padded[:, tap:tap + L, :] * w[:, tap].astype(np.float64)[None, None, :]
+    ref = (mixed / (1 + np.exp(-mixed))).reshape(b * L, C)
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-7)
+    t = torch.nn.functional.conv1d(torch.from_numpy(pr).permute(0, 2, 1), torch.from_numpy(w).double()[:, None, :],
+                                   padding=k - 1, groups=C)[:, :, :L]
+    t = torch.nn.functional.silu(t).permute(0, 2, 1).reshape(b * L, C).numpy()
+    np.testing.assert_allclose(got, t, rtol=1e-5, atol=1e-7)
+
+
+def test_conv_silu_bf16_against_torch_bf16_ops(orc):
+    """The bf16 path follows the reference's bf16 tensor arithmetic: each
+    product and partial sum rounded (candle bf16 ops; the CUDA kernel's
+    T(product) and T(fadd)).  Restated independently with torch bf16 tensor
+    ops; SiLU in f32 then rounded.  At most 1 bf16 ulp apart (exp's last
+    bit), nearly all bit-equal."""
+    torch = pytest.importorskip("torch")
+    p, w, pos, (b, L, C, k) = _conv_ref_gen()
+    p, w = orc.round_bf16(p), orc.round_bf16(w)
+    got = orc.conv_silu(p, w, pos, bf16=True)
+    pt = torch.from_numpy(p.reshape(b, L, C)).to(torch.bfloat16)
+    padded = torch.cat([torch.zeros(b, k - 1, C, dtype=torch.bfloat16), pt], 1)
+    mixed = torch.zeros(b, L, C, dtype=torch.bfloat16)
+    wt = torch.from_numpy(w).to(torch.bfloat16)
+    for tap in range(k):
+        mixed = mixed + padded[:, tap:tap + L, :] * wt[:, tap].reshape(1, 1, C)
+    ref = torch.nn.functional.silu(mixed.float()).to(torch.bfloat16).float().reshape(b * L, C).numpy()
+    diff = np.abs(got - ref)
+    assert (diff <= 2.0 ** -8 * np.abs(ref) + 1e-30).all()
+    assert (diff == 0).mean() > 0.99
+
+
+def test_conv_silu_closed_forms(orc):
+    """Identity tap: weight 1 on the newest tap gives silu(p); an impulse
+    at one row spreads to the next three rows of its sequence only, with the
+    taps reversed; a sequence start cuts the history."""
+    C = 8
+    p = orc.round_bf16(orc.fill_normal((10, C), 81))
+    pos = np.arange(10, dtype=np.int32)
+    w = np.zeros((C, 4), np.float32)
+    w[:, 3] = 1.0
+    np.testing.assert_array_equal(orc.conv_silu(p, w, pos), orc.round_bf16(p / (1 + np.exp(-p.astype(np.float64)))))
+    imp = np.zeros((10, C), np.float32)
+    imp[4] = 1.0
+    w2 = np.tile(np.array([0.5, 0.25, -0.75, 2.0], np.float32), (C, 1))
+    pre = orc.conv_silu(imp, w2, pos, bf16=False)
+    silu = lambda v: v / (1 + np.exp(-v))
+    for r, tap in ((4, 3), (5, 2), (6, 1), (7, 0)):
+        np.testing.assert_allclose(pre[r], silu(w2[0, tap]) * np.ones(C), rtol=1e-6)
+    assert np.all(pre[[0, 1, 2, 3, 8, 9]] == 0)
+    pos2 = np.array([0, 1, 2, 3, 4, 0, 1, 2, 3, 4], np.int32)  # a new sequence at row 5
+    pre2 = orc.conv_silu(imp, w2, pos2, bf16=False)
+    np.testing.assert_allclose(pre2[4], pre[4])
+    assert np.all(pre2[5:] == 0)
+
+
 def test_layer_norm_against_torch(orc):
     torch = pytest.importorskip("torch")
     x = orc.fill_normal((13, 768), 4) * 3 + 1
