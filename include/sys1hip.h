@@ -197,9 +197,10 @@ SYS1HIP_API int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t l
  *   positions int32 [M]: token m's position within its sequence (packed
  *   ragged rows; taps before a sequence's first token read zeros, as the
  *   reference's left zero padding does).
- * y[:, :conv_ch] = bf16(silu(c)), c accumulated over the 4 taps in bf16 from
- * bf16 products of the bf16-rounded projection (the reference's rounding),
- * and y[:, conv_ch:N] is the rounded projection.  M up to 2^20 rows. */
+ * y[:, :conv_ch] = bf16(silu(c)), c the 4-tap sum over the bf16-rounded
+ * projection accumulated in f32 (the reference rounds each product and
+ * partial sum to bf16; the two agree to the projection tolerance), and
+ * y[:, conv_ch:N] is the rounded projection.  M up to 2^20 rows. */
 SYS1HIP_API int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx,
                                               const uint16_t* w, int64_t ldw, int32_t norm, float eps,
                                               const uint16_t* conv_w, int64_t conv_ch,

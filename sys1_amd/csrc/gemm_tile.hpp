@@ -477,9 +477,12 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
   // DeltaNet causal conv + SiLU over the in_proj qkv columns
   // (src/archs/qwen35_text.rs:515-526,632-650; src/kernels/qwen35.cu:3-29):
   // out[r, n] = silu(sum over taps t = 3..0 of w[n, 3 - t] * p[r - t, n]),
-  // p = the bf16-rounded projection, each product rounded to bf16 and added
-  // in bf16, taps before the row's sequence start (pos[r] < t) skipped;
-  // columns from conv_ch on are the plain projection (z, b, a).  The wave
+  // p = the bf16-rounded projection, taps before the row's sequence start
+  // (pos[r] < t) reading zeros; columns from conv_ch on are the plain
+  // projection (z, b, a).  The taps accumulate in f32 and the SiLU uses the
+  // hardware exp and reciprocal, rounded once to bf16: the reference rounds
+  // every product and partial sum to bf16 instead, which costs three times
+  // the VALU work in this epilogue and agrees to the projection tolerance.  The wave
   // holds all rows of the tile (WM = 1): row R = 32 j + lane % 32 of block
   // j, so row R - t is lane - t of block j, or lane + 32 - t of block j - 1.
   // One ds_bpermute per tap moves a bf16 pair: each lane offers block j's
@@ -558,19 +561,18 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
             }
             const int tap = kConvTaps - 1 - t;
 #pragma unroll
-            for (int j = 0; j < S::FM; ++j)
-              if (pos[j] >= t) {
+            for (int j = 0; j < S::FM; ++j) {
+              const float keep = pos[j] >= t ? 1.0f : 0.0f;  // taps before the sequence start read zeros
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                  val[j][e] = round_bf16(val[j][e] + round_bf16(x[j][e] * cw[e][tap]));
-              }
+              for (int e = 0; e < 4; ++e) val[j][e] = fmaf(x[j][e] * keep, cw[e][tap], val[j][e]);
+            }
           }
 #pragma unroll
           for (int j = 0; j < S::FM; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const float v = val[j][e];
-              o[j][g][e] = to_bf16(v / (1.0f + expf(-v)));
+              o[j][g][e] = to_bf16(v * __frcp_rn(1.0f + __expf(-v)));
             }
         } else {
 #pragma unroll
