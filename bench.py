@@ -56,6 +56,9 @@ def parse():
     ap.add_argument("--norms", action="store_true",
                     help="fuse each projection's pre-norm (LayerNorm / RMSNorm) into it; the "
                          "row-statistics pass then sits inside the timed step")
+    ap.add_argument("--conv", action="store_true",
+                    help="fuse the DeltaNet causal conv + SiLU into each in_proj (Qwen3.5 stacks; "
+                         "positions from the packed batch's sequence lengths)")
     ap.add_argument("--graph", action="store_true",
                     help="replay one HIP graph per prepared batch instead of enqueueing every "
                          "projection from the host (measured: no difference on one MI355X)")
@@ -157,23 +160,26 @@ def main():
     cfg = CONFIGS[cfg_name]()
     if args.tokens:
         Ms = [args.tokens]
+        seqs = [np.array([args.tokens])]
         batch_desc = f"fixed M={args.tokens}"
     else:
         if lens is None:
             raise SystemExit(f"--workload {args.workload} needs --tokens")
-        Ms = [int(batching.draw_lengths(args.seed + b, lens[0], lens[1], budget, exact).sum())
-              for b in range(args.batches)]
+        seqs = [batching.draw_lengths(args.seed + b, lens[0], lens[1], budget, exact)
+                for b in range(args.batches)]
+        Ms = [int(l.sum()) for l in seqs]
         batch_desc = (f"lengths U[{lens[0]},{lens[1]}] packed to {budget}"
                       f"{' exactly' if exact else ''}, {args.batches} batches cycled")
     max_m = max(Ms)
 
     torch.cuda.set_device(0)
     dev = HipDevice(0)
-    stack = ProjectionStack(cfg, dev, max_m, seed=args.seed, norms=args.norms)
+    stack = ProjectionStack(cfg, dev, max_m, seed=args.seed, norms=args.norms, conv=args.conv)
     gen = torch.Generator(device="cuda:0")
     gen.manual_seed(args.seed + 1000)
     x = torch.randn(max_m, cfg.hidden, generator=gen, device="cuda:0").to(torch.bfloat16)
-    prepared = [stack.prepare(x, M) for M in Ms]
+    positions = [torch.from_numpy(batching.positions(l)).to("cuda:0") for l in seqs]
+    prepared = [stack.prepare(x, M, positions[b]) for b, M in enumerate(Ms)]
     torch.cuda.synchronize()
 
     for s in range(args.warmup):
@@ -245,7 +251,7 @@ def main():
                 e1.record()
                 if rc:
                     raise RuntimeError(f"launch failed: {rc}")
-                recs.append((p, a[10], e0, e1))
+                recs.append((p, Ms[s % len(Ms)], e0, e1))
         torch.cuda.synchronize()
         for p, M, e0, e1 in recs:
             d = per_proj.setdefault(p.name, {"n": 0, "ms": 0.0, "flop": 0, "bytes": 0,
@@ -316,6 +322,7 @@ def main():
                    "launch": "one HIP graph per prepared batch" if args.graph else "eager",
                    "pre_norms": "fused (row statistics + folded norm weights)" if args.norms
                    else "none (projections only)",
+                   "deltanet_conv": "fused into in_proj" if args.conv else "none",
                    "layers": len(cfg.layers), "hidden": cfg.hidden,
                    "packed_M": Ms, "flop_per_token": cfg.flops_per_token(),
                    "weight_bytes": cfg.weight_bytes(), "parallelism": "single GPU"},

@@ -193,7 +193,8 @@ SYS1HIP_API int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t l
  *   just the qkv rows, N = conv_ch); folded by sys1hip_fold_norm_weight when
  *   norm is set;
  *   conv_w bf16 [conv_ch, 4]: the conv1d weight [conv_ch, 1, 4], taps
- *   oldest first; conv_ch a multiple of 4;
+ *   oldest first; conv_ch a multiple of 8; y 16-byte aligned, ldy a
+ *   multiple of 8;
  *   positions int32 [M]: token m's position within its sequence (packed
  *   ragged rows; taps before a sequence's first token read zeros, as the
  *   reference's left zero padding does).

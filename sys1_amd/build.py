@@ -14,7 +14,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libsys1hip.so")
 SOURCES = [os.path.join(CSRC, "sys1hip.hip")]
-HEADERS = [os.path.join(CSRC, f) for f in ("common.hpp", "gemm_tile.hpp", "norm.hpp")] + [
+HEADERS = [os.path.join(CSRC, f) for f in ("common.hpp", "gemm_tile.hpp", "norm.hpp", "conv.hpp")] + [
     os.path.join(ROOT, "include", "sys1hip.h")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

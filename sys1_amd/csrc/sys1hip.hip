@@ -13,6 +13,7 @@
 #include "common.hpp"
 #include "gemm_tile.hpp"
 #include "norm.hpp"
+#include "conv.hpp"
 
 using namespace sys1;
 
@@ -648,9 +649,9 @@ int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx, con
   Context* c = static_cast<Context*>(ctx);
   if (norm != 0 && norm != SYS1HIP_NORM_RMS)
     return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: norm %d (0 or SYS1HIP_NORM_RMS)", norm);
-  if (M < 0 || N <= 0 || K <= 0 || conv_ch <= 0 || conv_ch > N || conv_ch % 4 || !(eps >= 0.0f))
+  if (M < 0 || N <= 0 || K <= 0 || conv_ch <= 0 || conv_ch > N || conv_ch % 8 || !(eps >= 0.0f))
     return fail(SYS1HIP_EINVAL,
-                "sys1hip_linear_conv_silu_bf16: bad shape M=%lld N=%lld K=%lld conv_ch=%lld (multiple of 4, "
+                "sys1hip_linear_conv_silu_bf16: bad shape M=%lld N=%lld K=%lld conv_ch=%lld (multiple of 8, "
                 "at most N) or eps",
                 (long long)M, (long long)N, (long long)K, (long long)conv_ch);
   if (M == 0) return SYS1HIP_OK;
@@ -667,21 +668,11 @@ int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx, con
                 (long long)M, (long long)kNormRows);
   if (N > (1ll << 30) || K > (1ll << 30))
     return fail(SYS1HIP_ERANGE, "sys1hip_linear_conv_silu_bf16: dimension above 2^30");
+  if (ldy % 8 || !aligned16(y))
+    return fail(SYS1HIP_EALIGN, "sys1hip_linear_conv_silu_bf16: y must be 16-byte aligned, ldy a multiple of 8");
   int rc = use_device(c);
   if (rc) return rc;
-  const int epi = norm ? kEpiNormRmsConvSilu : kEpiConvSilu;
-  const Plan p = resolve(c, M, N, K, false, true);
-  const KernelEntry& e = kKernels[p.kernel];
-  if (!e.fn[epi])
-    return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: kernel %s has no conv epilogue", e.name);
-  const int64_t rows = halo_rows(e, M, kConvHalo);
-  if (e.streamk && (cdiv(rows, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
-    return fail(SYS1HIP_ERANGE, "sys1hip_linear_conv_silu_bf16: more split tiles than stream-K counters");
   const auto* xb = reinterpret_cast<const __bf16*>(x);
-  if (norm) {
-    rc = launch_row_stats(c, xb, ldx, M, K, norm, eps);
-    if (rc) return rc;
-  }
   GemmArgs a = {};
   a.x = xb;
   a.w = reinterpret_cast<const __bf16*>(w);
@@ -690,12 +681,51 @@ int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx, con
   a.counters = c->counters;
   a.ldx = ldx, a.ldw = ldw, a.ldr = 0, a.ldy = ldy;
   a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)N;
-  a.dp_tiles = (int)std::min<int64_t>(p.dp, 1 << 30);
   a.stats = c->stats;
   a.pos = positions;
   a.conv_w = reinterpret_cast<const __bf16*>(conv_w);
   a.conv_ch = (int)conv_ch;
+  // Two forms.  Fused: the conv in the GEMM epilogue, on the shapes whose
+  // waves span every row of a tile (chosen when such a kernel is forced).
+  // Two-pass (the default): the projection on the best kernel for the
+  // shape, then the conv in place over segments of rows.  On MI355X the
+  // two-pass form measured faster at M = 128 and 8192: the wave-spanning
+  // shapes lose more in the GEMM than the fused form saves in traffic.
+  const bool fused = c->forced_kernel >= 0 && kKernels[c->forced_kernel].wm == 1;
+  const int epi = fused ? (norm ? kEpiNormRmsConvSilu : kEpiConvSilu) : (norm ? kEpiNormRms : kEpiNone);
+  const Plan p = resolve(c, M, N, K, false, fused);
+  const KernelEntry& e = kKernels[p.kernel];
+  if (!e.fn[epi])
+    return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: kernel %s has no conv epilogue", e.name);
+  const int64_t rows = fused ? halo_rows(e, M, kConvHalo) : M;
+  if (e.streamk && (cdiv(rows, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
+    return fail(SYS1HIP_ERANGE, "sys1hip_linear_conv_silu_bf16: more split tiles than stream-K counters");
+  if (norm) {
+    rc = launch_row_stats(c, xb, ldx, M, K, norm, eps);
+    if (rc) return rc;
+  }
+  a.dp_tiles = (int)std::min<int64_t>(p.dp, 1 << 30);
   hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)p.grid), dim3(e.threads), 0, c->stream, a);
+  HIP_TRY(hipGetLastError());
+  if (fused) return SYS1HIP_OK;
+  // Segments of S rows, one chunk (kConvChunk) each for the most threads
+  // in flight (measured: 64-row segments left the pass latency-bound at
+  // 8192 tokens), longer only when the saved halos (kConvHalo rows of
+  // conv_ch bf16 per segment) would not fit the workspace.
+  const int64_t vecs = conv_ch / kConvVec;
+  const int64_t halo_row_bytes = (int64_t)kConvHalo * conv_ch * 2;
+  const int64_t max_segs = std::max<int64_t>(1, (int64_t)kWorkspaceBytes / halo_row_bytes);
+  const int64_t S = std::max<int64_t>(kConvChunk, cdiv(cdiv(M, max_segs), kConvChunk) * kConvChunk);
+  const int64_t segs = cdiv(M, S);
+  auto* halo = reinterpret_cast<__bf16*>(c->ws);
+  if (segs > 1) {
+    const int64_t n = (segs - 1) * kConvHalo * vecs;
+    hipLaunchKernelGGL(conv_halo_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, c->stream, a.y, ldy, (int)M,
+                       (int)conv_ch, (int)S, halo);
+    HIP_TRY(hipGetLastError());
+  }
+  hipLaunchKernelGGL(conv_silu_inplace_kernel, dim3((unsigned)cdiv(segs * vecs, 256)), dim3(256), 0, c->stream,
+                     a.y, ldy, (int)M, (int)conv_ch, (int)S, halo, a.conv_w, positions);
   HIP_TRY(hipGetLastError());
   return SYS1HIP_OK;
 }

@@ -35,8 +35,8 @@ class InProjConv:
                  device: HipDevice | None = None):
         self.device = device or load_device(weight.device.index or 0)
         _check_operand(weight, "weight", self.device)
-        if weight.dim() != 2 or not (0 < conv_channels <= weight.shape[0]) or conv_channels % 4:
-            raise ValueError(f"conv_channels must be a multiple of 4 in (0, {weight.shape[0]}], "
+        if weight.dim() != 2 or not (0 < conv_channels <= weight.shape[0]) or conv_channels % 8:
+            raise ValueError(f"conv_channels must be a multiple of 8 in (0, {weight.shape[0]}], "
                              f"got {conv_channels}")
         cw = conv_weight.reshape(conv_channels, -1)
         if cw.shape[1] != 4:

@@ -43,6 +43,7 @@ class Proj:
     dst: str        # output buffer name
     resid: str | None = None
     norm: str | None = None  # pre-norm of the input ("layer" / "rms"), fused when the stack has norms
+    conv_ch: int = 0         # leading output columns under the DeltaNet causal conv + SiLU
 
     @property
     def nout(self) -> int:
@@ -108,7 +109,8 @@ def qwen35(hidden: int, layers: int, heads: int, kv_heads: int, head_dim: int,
     ]
     dn_in = 2 * dn_qk + 2 * dn_v + 2 * dn_heads  # qkv | z | b | a
     deltanet = [
-        Proj("in_proj_qkvzba", H, dn_in, _lib.EPI_NONE, "h", 0, "mix", norm="rms"),
+        Proj("in_proj_qkvzba", H, dn_in, _lib.EPI_NONE, "h", 0, "mix", norm="rms",
+             conv_ch=2 * dn_qk + dn_v),
         Proj("out_proj", dn_v, H, _lib.EPI_RESIDUAL, "mix", 2 * dn_qk + dn_v, "h", resid="h"),
     ] + mlp
     q_w = 2 * heads * head_dim
@@ -149,12 +151,17 @@ class ProjectionStack:
     (sys1hip_norm_linear_bf16) with the norm weights of a fresh model --
     LayerNorm weight 1, RMSNorm weight 0 (alpha 1) -- or `norm_weights`
     [layer][projection] (f32 [K] or None), with eps per kind (NORM_EPS, or
-    `norm_eps`).  norms=False runs the projections alone."""
+    `norm_eps`).  norms=False runs the projections alone.
+
+    conv=True fuses the DeltaNet causal conv + SiLU into each in_proj
+    (Proj.conv_ch columns; conv weights N(0, 0.5^2) or `conv_weights`
+    [layer] -> [conv_ch, 4]); the calls then need per-token positions."""
 
     def __init__(self, cfg: StackConfig, dev: HipDevice, max_tokens: int, seed: int = 0,
                  weights: list[list[torch.Tensor]] | None = None, w_std: float = 0.02,
                  norms: bool = False, norm_weights: list[list[torch.Tensor | None]] | None = None,
-                 norm_eps: dict[str, float] | None = None):
+                 norm_eps: dict[str, float] | None = None, conv: bool = False,
+                 conv_weights: list[torch.Tensor | None] | None = None):
         self.cfg = cfg
         self.dev = dev
         self.max_tokens = max_tokens
@@ -164,6 +171,8 @@ class ProjectionStack:
         from .linear import pack_gated_weight
         from .norm import fold_norm_weight
         self.norms = norms
+        self.conv = conv
+        self.conv_w: list[torch.Tensor | None] = []
         self.norm_eps = dict(NORM_EPS, **(norm_eps or {}))
         self.weights: list[list[torch.Tensor]] = []
         self.colsums: list[list[torch.Tensor | None]] = []
@@ -187,6 +196,14 @@ class ProjectionStack:
                 cs.append(c)
             self.weights.append(ws)
             self.colsums.append(cs)
+            cwt = None
+            convs = [p for p in layer if p.conv_ch]
+            if conv and convs:
+                cwt = conv_weights[li] if conv_weights is not None else None
+                if cwt is None:
+                    cwt = torch.randn(convs[0].conv_ch, 4, generator=g, device=d) * 0.5
+                cwt = cwt.reshape(convs[0].conv_ch, 4).to(device=d, dtype=torch.bfloat16).contiguous()
+            self.conv_w.append(cwt)
         widths: dict[str, int] = {"h": cfg.hidden}
         for layer in cfg.layers:
             for p in layer:
@@ -196,8 +213,9 @@ class ProjectionStack:
                         for k, v in widths.items()}
         self._fn = dev._L.sys1hip_linear_bf16
         self._norm_fn = dev._L.sys1hip_norm_linear_bf16
+        self._conv_fn = dev._L.sys1hip_linear_conv_silu_bf16
 
-    def _calls(self, x: torch.Tensor, M: int) -> list[tuple]:
+    def _calls(self, x: torch.Tensor, M: int, positions: torch.Tensor | None = None) -> list[tuple]:
         """Argument tuples of every launch for M tokens (prepared once per M,
         so the enqueue loop is a plain sequence of C calls)."""
         assert x.shape[1] == self.cfg.hidden and x.dtype == torch.bfloat16 and x.stride(1) == 1
@@ -225,7 +243,15 @@ class ProjectionStack:
                     else:
                         rptr, ldr = bufs["h"].data_ptr(), bufs["h"].stride(0)
                 w = self.weights[li][pi]
-                if self.norms and p.norm:
+                if self.conv and p.conv_ch:
+                    if positions is None or positions.numel() < M or positions.dtype != torch.int32:
+                        raise ValueError("a stack with the conv fused needs int32 positions for every row")
+                    normed = self.norms and p.norm == "rms"
+                    calls.append((p, self._conv_fn, (
+                        src, ldx, w.data_ptr(), w.stride(0), _lib.NORM_RMS if normed else 0,
+                        self.norm_eps["rms"], self.conv_w[li].data_ptr(), p.conv_ch,
+                        positions.data_ptr(), dst.data_ptr(), dst.stride(0), M, p.N, p.K)))
+                elif self.norms and p.norm:
                     c = self.colsums[li][pi]
                     calls.append((p, self._norm_fn, (
                         src, ldx, w.data_ptr(), w.stride(0), c.data_ptr() if c is not None else None,
@@ -236,12 +262,13 @@ class ProjectionStack:
                                                 dst.data_ptr(), dst.stride(0), M, p.N, p.K, p.epi)))
         return calls
 
-    def prepare(self, x: torch.Tensor, M: int):
+    def prepare(self, x: torch.Tensor, M: int, positions: torch.Tensor | None = None):
         """[(projection, C function, argument tuple)] of every launch."""
         ctx = self.dev.ctx
         out = []
-        for p, fn, args in self._calls(x, M):
-            ptrs = (0, 2, 4, 7) if fn is self._norm_fn else (0, 2, 4, 5, 7)
+        for p, fn, args in self._calls(x, M, positions):
+            ptrs = ((0, 2, 4, 7) if fn is self._norm_fn else (0, 2, 6, 8, 9) if fn is self._conv_fn
+                    else (0, 2, 4, 5, 7))
             out.append((p, fn, (ctx, *[ctypes.c_void_p(a) if i in ptrs and a is not None else a
                                       for i, a in enumerate(args)])))
         return out
@@ -252,9 +279,9 @@ class ProjectionStack:
             if rc:
                 _lib.check(rc, self.dev.ctx)
 
-    def forward(self, x: torch.Tensor, M: int) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, M: int, positions: torch.Tensor | None = None) -> torch.Tensor:
         """Enqueue the whole stack for the first M rows of x; returns the
         hidden-state buffer (first M rows valid once the stream reaches it)."""
         self.dev.follow_torch_stream()
-        self.run_prepared(self.prepare(x, M))
+        self.run_prepared(self.prepare(x, M, positions))
         return self.buffers["h"][:M, :self.cfg.hidden]

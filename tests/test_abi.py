@@ -208,13 +208,14 @@ def _conv(ctx=_ctx, x=_P, ldx=64, w=_P, ldw=64, norm=0, eps=1e-6, cw=_P, C=64, p
     (dict(norm=_lib.NORM_LAYER), _lib.EINVAL),     # RMSNorm only (Qwen3.5)
     (dict(C=0), _lib.EINVAL),
     (dict(C=130), _lib.EINVAL),                    # more conv channels than N
-    (dict(C=62), _lib.EINVAL),                     # multiple of 4
+    (dict(C=60), _lib.EINVAL),                     # multiple of 8
     (dict(M=-1), _lib.EINVAL),
     (dict(pos=None), _lib.EINVAL),
     (dict(cw=None), _lib.EINVAL),
     (dict(ldy=64), _lib.EINVAL),
     (dict(K=60, ldx=64, ldw=64), _lib.EALIGN),
     (dict(cw=_P + 8), _lib.EALIGN),
+    (dict(ldy=132), _lib.EALIGN),
     (dict(M=(1 << 20) + 1), _lib.ERANGE),
 ])
 def test_conv_rejects_bad_arguments(kwargs, code):

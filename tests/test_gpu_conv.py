@@ -126,8 +126,9 @@ def test_inproj_conv_matches_oracle(dev, orc, M, N, C, K, norm):
 
 
 def test_every_conv_kernel_and_grid(dev, orc):
-    """Each kernel with a conv epilogue, forced, over several grids (tile
-    rows split across workgroups, stream-K partial tiles)."""
+    """The fused form: each kernel with a conv epilogue, forced, over
+    several grids (tile rows split across workgroups, stream-K partial
+    tiles)."""
     from sys1_amd import kernel_names
     M, N, C, K = 700, 544, 384, 328
     x, w, cw, g, pos = _case(orc, M, N, C, K, 7, False)
@@ -146,12 +147,29 @@ def test_every_conv_kernel_and_grid(dev, orc):
         dev.set_grid(0)
 
 
-def test_conv_rejects_kernels_without_conv_epilogue(dev, orc):
-    from sys1_amd import _lib, kernel_names
-    x, w, cw, g, pos = _case(orc, 64, 256, 128, 64, 3, False)
+def test_two_pass_on_a_forced_tile_kernel(dev, orc):
+    """A forced kernel without the conv epilogue runs the two-pass form (its
+    projection, then the in-place conv): the same checks."""
+    from sys1_amd import kernel_names
+    M, N, C, K = 520, 544, 256, 264
+    x, w, cw, g, pos = _case(orc, M, N, C, K, 3, True)
     try:
         dev.set_kernel(kernel_names().index("tile_128x128_s2_w2x2"))
-        with pytest.raises(_lib.Sys1HipError):
-            _run(dev, x, w, cw, g, pos, 128)
+        y = _run(dev, x, w, cw, g, pos, C)
+        _check(orc, dev, y, x, w, cw, g, pos, C, "two-pass on tile_128x128_s2_w2x2")
     finally:
         dev.set_kernel(-1)
+
+
+def test_two_pass_segments_and_halos(dev, orc):
+    """Rows cut into many conv segments (M well above the 64-row segment),
+    sequence starts on and next to segment boundaries."""
+    from sys1_amd import batching
+    M, N, C, K = 1000, 288, 256, 64
+    x = orc.round_bf16(orc.fill_normal((M, K), 51))
+    w = orc.round_bf16(orc.fill_normal((N, K), 52, 0.1))
+    cw = orc.round_bf16(orc.fill_normal((C, 4), 53, 0.5))
+    cuts = sorted({0, 64, 127, 128, 129, 190, 192, 256, 511, 512, 700, 703, M})
+    pos = batching.positions(np.diff(cuts))
+    y = _run(dev, x, w, cw, None, pos, C)
+    _check(orc, dev, y, x, w, cw, None, pos, C, "segments")

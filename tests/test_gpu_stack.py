@@ -461,3 +461,45 @@ def test_stack_with_norms_from_safetensors_checkpoint(dev, orc, tmp_path):
     rel, _ = parity(to_np(out), h)
     print(f"[gpu] checkpoint stack with norms vs f32 oracle: rel_fro={rel:.3e}", flush=True)
     assert rel < CHAIN_TOL
+
+
+def test_qwen_stack_with_norms_and_conv_matches_f32_chain(dev, orc):
+    """The Qwen3.5 stack with its input RMSNorms and the DeltaNet causal
+    conv + SiLU fused into in_proj (ProjectionStack(norms=True, conv=True))
+    on ragged packed sequences, against the f32 chain with both unfused
+    (src/archs/qwen35_text.rs:515-526,632-650,932-940)."""
+    from sys1_amd import batching
+    from sys1_amd.stacks import ProjectionStack, qwen35
+    cfg = qwen35(2048, 4, 16, 2, 128, 6144, 2048, 4096, 16, 2048, "qwen35-small-4")
+    lengths = batching.draw_lengths(21, 16, 300, 700)
+    M = int(lengths.sum())
+    pos = batching.positions(lengths)
+    print(f"[gpu] qwen stack norms+conv M={M} ({len(lengths)} sequences)", flush=True)
+    x = orc.fill_normal((M, cfg.hidden), 23)
+    ws = _weights(orc, cfg, 700)
+    cws = [orc.round_bf16(orc.fill_normal((layer[0].conv_ch, 4), 900 + li, 0.5)) if layer[0].conv_ch else None
+           for li, layer in enumerate(cfg.layers)]
+    stack = ProjectionStack(cfg, dev, M, weights=[[to_gpu_bf16(w, torch) for w in l] for l in ws],
+                            norms=True, conv=True,
+                            conv_weights=[torch.from_numpy(c) if c is not None else None for c in cws])
+    h_gpu = to_np(stack.forward(to_gpu_bf16(x, torch), M, torch.from_numpy(pos).cuda()))
+    torch.cuda.synchronize()
+    h = x.astype(np.float32)
+    mix = None
+    for li, layer in enumerate(cfg.layers):
+        for pi, p in enumerate(layer):
+            if p.src == "h":
+                src = orc.rms_norm(h, np.zeros(h.shape[-1], np.float32), 1e-6) if p.norm else h
+            else:
+                src = np.ascontiguousarray(mix[:, p.src_off:p.src_off + p.K])
+            out = _project_ref(orc, p, src, ws[li][pi], h if p.resid else None)
+            if p.conv_ch:
+                out = np.concatenate([orc.conv_silu(out[:, :p.conv_ch], cws[li], pos, bf16=False),
+                                      out[:, p.conv_ch:]], axis=1)
+            if p.dst == "h":
+                h = out
+            else:
+                mix = out
+    rel, mx = parity(h_gpu, h)
+    print(f"[gpu] qwen norms+conv final hidden vs f32 chain: rel_fro={rel:.3e} max={mx:.3e}", flush=True)
+    assert rel < CHAIN_TOL and mx < 5 * CHAIN_TOL
