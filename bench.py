@@ -62,6 +62,9 @@ def parse():
     ap.add_argument("--graph", action="store_true",
                     help="replay one HIP graph per prepared batch instead of enqueueing every "
                          "projection from the host (measured: no difference on one MI355X)")
+    ap.add_argument("--kernel", default=None, metavar="NAME",
+                    help="force one tile kernel (a sys1hip_kernel_name) for every projection, "
+                         "for tuning the kernel choice; the line then records it in config")
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="after the run, 8 bf16 negations of MIB MiB (read MIB, write MIB): the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -174,6 +177,9 @@ def main():
 
     torch.cuda.set_device(0)
     dev = HipDevice(0)
+    if args.kernel:
+        from sys1_amd import kernel_names
+        dev.set_kernel(kernel_names().index(args.kernel))
     stack = ProjectionStack(cfg, dev, max_m, seed=args.seed, norms=args.norms, conv=args.conv)
     gen = torch.Generator(device="cuda:0")
     gen.manual_seed(args.seed + 1000)
@@ -320,6 +326,7 @@ def main():
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) random-init weights)",
         "config": {"workload": f"{cfg.name} projection stack: {cfg.description}; {batch_desc}",
                    "launch": "one HIP graph per prepared batch" if args.graph else "eager",
+                   **({"forced_kernel": args.kernel} if args.kernel else {}),
                    "pre_norms": "fused (row statistics + folded norm weights)" if args.norms
                    else "none (projections only)",
                    "deltanet_conv": "fused into in_proj" if args.conv else "none",

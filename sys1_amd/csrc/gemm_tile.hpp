@@ -253,14 +253,19 @@ struct TileWalk {
 // STREAMK: stream-K schedule (the weight-streaming shapes); the large-M
 // shapes compile the tile schedule only.
 // OCC: resident workgroups per CU the register allocation must allow.
-template <int BM, int BN, int WM, int WN, int STAGES, int BK_, int OCC, bool STREAMK, int EPI>
-__global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a) {
+// PW: producer waves.  0: every wave issues its share of the refills between
+// its MFMAs.  PW > 0: PW extra waves issue all of them and do nothing else,
+// so a refill instruction that stalls issue while the load path drains
+// stalls no matrix work (tile schedule only).
+template <int BM, int BN, int WM, int WN, int STAGES, int BK_, int OCC, bool STREAMK, int EPI, int PW = 0>
+__global__ __launch_bounds__((WM * WN + PW) * 64, OCC) void gemm_tile_kernel(GemmArgs a) {
   using S = TileShape<BM, BN, WM, WN, STAGES, BK_>;
   constexpr int BK = S::BK;
   __shared__ __attribute__((aligned(1024))) char lds[S::kLdsBytes];
 
   constexpr bool kConv = epi_base(EPI) == kEpiConvSilu;
   static_assert(!kConv || WM == 1, "conv epilogue: one wave row per tile");
+  static_assert(PW == 0 || (!STREAMK && !kConv), "producer waves: plain tile schedule");
   const TileWalk walk(a.M, a.N, a.K, BM, BN, BK, STREAMK ? a.dp_tiles : 1 << 30, kConv ? kConvHalo : 0);
   if (walk.steps() == 0) return;
 
@@ -283,17 +288,21 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
   // source offsets (row clamp included) are computed when the issue cursor
   // enters a tile; a k-tile then costs only the scalar base advance, and the
   // K-tail test runs on a tile's last, partial k-tile only.
-  static_assert(S::XT % S::kWaves == 0, "x and w instructions split evenly per wave");
-  constexpr int kXDma = S::XT / S::kWaves;
+  constexpr int kDW = PW ? PW : S::kWaves;  // waves that issue refills
+  constexpr int kDma = S::DT / kDW;          // refill instructions per issuing wave per k-tile
+  static_assert(S::XT % kDW == 0 && S::DT % kDW == 0, "x and w instructions split evenly per wave");
+  static_assert(kDma * (STAGES - 1) < 64, "vmcnt field");
+  constexpr int kXDma = S::XT / kDW;
+  const int dwave = PW ? wave - S::kWaves : wave;
   auto dma_row = [&](int i) {
-    const int u = i * S::kWaves + wave;
+    const int u = i * kDW + dwave;
     return (i < kXDma ? u : u - S::XT) * S::RPI + lrow;
   };
-  unsigned src_off[S::kDma];
+  unsigned src_off[kDma];
   auto set_offsets = [&](const Segment& sg) {
     const int x_left = a.M - 1 - walk.row0(sg.tm), w_left = a.N - 1 - sg.tn * BN;
 #pragma unroll
-    for (int i = 0; i < S::kDma; ++i) {
+    for (int i = 0; i < kDma; ++i) {
       const int r = dma_row(i);
       const int c = lpos ^ lds_swz<BK>(r);
       src_off[i] = i < kXDma ? (unsigned)(min(r, x_left) * (int)a.ldx * 2 + c * 16)
@@ -328,7 +337,7 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
   auto dma_one = [&](const Refill& r, int i) {
     unsigned off = src_off[i];
     if (r.kleft < BK && (lpos ^ lds_swz<BK>(dma_row(i))) * 8 >= r.kleft) off = kOutOfRange;
-    dma16(i < kXDma ? r.xr : r.wr, off, (lds_void*)(r.base + (i * S::kWaves + wave) * 1024));
+    dma16(i < kXDma ? r.xr : r.wr, off, (lds_void*)(r.base + (i * kDW + dwave) * 1024));
   };
   auto issue_advance = [&]() {
     if (++is_kt == isg.kt1) {
@@ -340,9 +349,37 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
   auto issue = [&](int stage) {  // issue the cursor's k-tile, then advance the cursor
     const Refill r = refill_at(stage, true);
 #pragma unroll
-    for (int i = 0; i < S::kDma; ++i) dma_one(r, i);
+    for (int i = 0; i < kDma; ++i) dma_one(r, i);
     issue_advance();
   };
+
+  // ---- producer waves: the prologue's requests, then per k-tile: wait for
+  // the next k-tile's loads, the barrier that retires the current one (the
+  // compute waves' barrier, one per k-tile on both sides), then the refill
+  // of the stage it freed.
+  if constexpr (PW > 0) {
+    if (wave >= S::kWaves) {
+      const int steps = walk.steps();
+      for (int t = 0; t < STAGES; ++t)
+        if (t < steps) issue(t);
+      if (steps >= STAGES) vm_wait<(STAGES - 1) * kDma>();
+      else vm_wait<0>();
+      __syncthreads();
+      int stage = 0;
+      for (int s = 0; s < steps; ++s) {
+        if (s + 1 < steps) {
+          if (s + STAGES - 1 < steps) vm_wait<(STAGES - 2) * kDma>();
+          else vm_wait<0>();
+        }
+        __syncthreads();
+        const int freed = stage;
+        stage = stage + 1 == STAGES ? 0 : stage + 1;
+        if (s + STAGES < steps) issue(freed);
+      }
+      vm_wait<0>();
+      return;
+    }
+  }
 
   // ---- fragment addressing (byte offsets within a stage): lane reads row
   // (base + lane%32) of chunk 2*ks + lane/32.
@@ -792,10 +829,13 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
   // below: the next k-step's fragment reads are issued before the current
   // k-step's MFMAs, so LDS latency hides behind a full k-step of matrix work.
   const int steps = walk.steps();
-  for (int t = 0; t < STAGES; ++t)
-    if (t < steps) issue(t);
-  if (steps >= STAGES) vm_wait<(STAGES - 1) * S::kDma>();
-  else vm_wait<0>();
+  constexpr bool kIssue = PW == 0;  // this wave issues refills
+  if constexpr (kIssue) {
+    for (int t = 0; t < STAGES; ++t)
+      if (t < steps) issue(t);
+    if (steps >= STAGES) vm_wait<(STAGES - 1) * kDma>();
+    else vm_wait<0>();
+  }
   __syncthreads();
 
   Segment csg = walk.first_segment();  // compute cursor
@@ -809,7 +849,8 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
   //     stage's refill issued between them;
   //   otherwise (ping-pong sets): one k-step of MFMAs after the barrier.
   constexpr int kReads = S::FM + S::FN;  // LDS reads per fragment set
-  constexpr bool kDeep = S::KS == 4 && kReads * 4 * 4 <= 64;
+  constexpr int kWavesPerSimd = ((S::kWaves + PW) * OCC + 3) / 4;  // register budget 512 / this
+  constexpr bool kDeep = S::KS == 4 && kReads * 4 * 4 <= 64 && kWavesPerSimd <= 3;
   constexpr int kSets = kDeep ? 4 : 2;
   Frags fr[kSets];
   if (steps > 0) {
@@ -845,8 +886,8 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (s + 1 < steps) {
-      if (s + STAGES - 1 < steps) vm_wait<(STAGES - 2) * S::kDma>();
+    if (kIssue && s + 1 < steps) {
+      if (s + STAGES - 1 < steps) vm_wait<(STAGES - 2) * kDma>();
       else vm_wait<0>();
     }
     __syncthreads();
@@ -861,21 +902,21 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
     // other workgroup's MFMAs cover the refill, and one burst after the
     // first MFMA group measured faster.
     using std::integral_constant;
-    constexpr bool kSpread = OCC == 1;
+    constexpr bool kSpread = OCC == 1 && kIssue;
     const Refill r = refill_at(freed, s + STAGES < steps);
     auto refill_all = [&]() {
 #pragma unroll
-      for (int i = 0; i < S::kDma; ++i) dma_one(r, i);
+      for (int i = 0; i < kDma; ++i) if constexpr (kIssue) dma_one(r, i);
     };
     if constexpr (kDeep && kSpread) {
-      constexpr int kHalf = S::kDma / 2;
+      constexpr int kHalf = kDma / 2;
       if (s + 1 < steps) {
         read(fr[0], stage, 0);
         read(fr[1], stage, 1);
       }
       __builtin_amdgcn_sched_barrier(0);
       mma_dma(fr[2], r, integral_constant<int, 0>(), integral_constant<int, kHalf>());
-      mma_dma(fr[3], r, integral_constant<int, kHalf>(), integral_constant<int, S::kDma - kHalf>());
+      mma_dma(fr[3], r, integral_constant<int, kHalf>(), integral_constant<int, kDma - kHalf>());
     } else if constexpr (kDeep) {
       if (s + 1 < steps) read(fr[0], stage, 0);
       __builtin_amdgcn_sched_barrier(0);
@@ -889,7 +930,7 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
     } else if constexpr (kSpread) {
       if (s + 1 < steps) read(fr[0], stage, 0);
       __builtin_amdgcn_sched_barrier(0);
-      mma_dma(fr[(S::KS - 1) % 2], r, integral_constant<int, 0>(), integral_constant<int, S::kDma>());
+      mma_dma(fr[(S::KS - 1) % 2], r, integral_constant<int, 0>(), integral_constant<int, kDma>());
     } else {
       if (s + 1 < steps) read(fr[0], stage, 0);
       __builtin_amdgcn_sched_barrier(0);
@@ -897,7 +938,7 @@ __global__ __launch_bounds__(WM* WN * 64, OCC) void gemm_tile_kernel(GemmArgs a)
       __builtin_amdgcn_sched_barrier(0);
       refill_all();
     }
-    if (s + STAGES < steps) issue_advance();
+    if (kIssue && s + STAGES < steps) issue_advance();
     __builtin_amdgcn_sched_barrier(0);
     if (++ckt == csg.kt1) {
       if constexpr (STREAMK) {

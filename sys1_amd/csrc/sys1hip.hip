@@ -9,6 +9,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "common.hpp"
 #include "gemm_tile.hpp"
@@ -54,6 +55,9 @@ struct Context {
   int forced_grid = 0;
   int forced_dp = -1;
   int cus = 256;
+  // Resident workgroups per CU of each (kernel, epilogue) as the runtime
+  // reports them (an epilogue that needs more registers can fit fewer).
+  std::vector<int> occ;
 };
 
 using KernelFn = void (*)(GemmArgs);
@@ -69,42 +73,46 @@ struct KernelEntry {
   int stages;           // LDS pipeline stages (stages - 1 k-tiles in flight)
   int tn;               // output columns per wave (the RoPE epilogue needs 64: one head)
   int wm;               // waves along M (the conv epilogue needs 1: a wave holds every row)
+  int pw;               // producer waves (0: the compute waves issue the refills)
   KernelFn fn[kEpiCount];
 };
 
 // The conv epilogues exist for shapes whose waves hold every row of a tile.
-template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK, int EPI>
+template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK, int EPI, int PW>
 constexpr KernelFn conv_fn() {
-  if constexpr (WM == 1) return gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, EPI>;
+  if constexpr (WM == 1 && PW == 0) return gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, EPI, PW>;
   else return nullptr;
 }
 
-template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK>
+// PW: producer waves (see gemm_tile_kernel).
+template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK, int PW = 0>
 constexpr KernelEntry tile_entry(const char* name, float eff) {
-  return KernelEntry{name, BM, BN, WM * WN * 64, OCC, SK, eff, BK, ST, BN / WN, WM,
-                     {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 0>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 1>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 2>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 3>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 4>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 5>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 6>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 7>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 8>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 9>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 10>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 11>,
-                      conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 12>(),
-                      conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 13>()}};
+  return KernelEntry{name, BM, BN, (WM * WN + PW) * 64, OCC, SK, eff, BK, ST, BN / WN, WM, PW,
+                     {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 0, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 1, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 2, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 3, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 4, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 5, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 6, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 7, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 8, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 9, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 10, PW>,
+                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 11, PW>,
+                      conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 12, PW>(),
+                      conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 13, PW>()}};
 }
 
 // Output-tile shapes.  The first group serves large M (MFMA-bound); the
 // "stream" group serves small M (weight-streaming: BM = padded token count,
 // BN = 256, deep stages, K split over workgroups).
 const KernelEntry kKernels[] = {
+    // Large M.  _p4: four producer waves issue the refills (see gemm_tile_kernel).
     tile_entry<256, 256, 2, 4, 2, 64, 1, false>("tile_256x256_s2_w2x4", 0.80f),
-    tile_entry<128, 256, 2, 4, 2, 64, 1, false>("tile_128x256_s2_w2x4", 0.40f),
-    tile_entry<128, 192, 4, 2, 2, 64, 1, false>("tile_128x192_s2_w4x2", 0.40f),
+    tile_entry<128, 256, 2, 4, 3, 64, 1, false, 4>("tile_128x256_s3_w2x4_p4", 0.50f),
+    tile_entry<256, 128, 2, 2, 3, 64, 1, false, 4>("tile_256x128_s3_w2x2_p4", 0.74f),
+    tile_entry<128, 128, 2, 2, 2, 64, 2, false, 4>("tile_128x128_s2_w2x2_p4", 0.70f),
     tile_entry<128, 128, 2, 2, 2, 64, 2, false>("tile_128x128_s2_w2x2", 0.60f),
     tile_entry<32, 256, 1, 4, 4, 64, 1, true>("stream_32x256_s4_w1x4", 0.50f),
     tile_entry<64, 256, 2, 4, 3, 64, 1, true>("stream_64x256_s3_w2x4", 0.60f),
@@ -150,9 +158,16 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 constexpr double kFlopPerClk = 4096.0;      // bf16 MFMA per CU per clock
 constexpr double kLoadBytesPerClk = 48.0;   // L2 -> LDS per CU
 constexpr double kStoreBytesPerClk = 64.0;
+// A tile kernel's epilogue: output bytes at this rate, twice the time for an
+// epilogue other than the plain store (operand reads, gating), half of it
+// hidden when another workgroup on the CU runs MFMAs meanwhile.
+constexpr double kTileStoreBytesPerClk = 32.0;
 constexpr double kHbmBytesPerClk = 1500.0;  // whole chip, sustained by a weight stream
 constexpr double kFixupClk = 2000.0;        // partial write + arrival
 constexpr double kLatencyClk = 1500.0;      // load issue -> data in LDS
+// With producer waves a refill is issued as soon as its stage is freed, not
+// behind the compute waves' MFMAs: a shorter effective latency.
+constexpr double kProducerLatencyClk = 900.0;
 
 struct Plan {
   int kernel = 0;
@@ -161,15 +176,32 @@ struct Plan {
   double cost = 1e300;
 };
 
-double model_cost(const Context* c, const KernelEntry& e, int64_t M, int64_t N, int64_t K,
+int occupancy(const Context* c, int id, int epi) {
+  const int n = c->occ.empty() ? 0 : c->occ[(size_t)id * kEpiCount + epi];
+  return n > 0 ? std::min(n, kKernels[id].occupancy) : kKernels[id].occupancy;
+}
+
+// A kernel whose epilogue variant fits fewer workgroups per CU than its
+// shape was fitted with loses the overlap between them: 0.7 of the rate
+// (measured: the 128x128 producer-wave shape with a LayerNorm epilogue at
+// one workgroup per CU against the plain shape at two).
+constexpr double kLowOccupancyRate = 0.7;
+
+double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64_t K,
                   int64_t grid, int64_t dp) {
+  const KernelEntry& e = kKernels[id];
   const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
   const int64_t kts = cdiv(K, e.bk);
   const double share = std::max(1.0, (double)grid / c->cus);  // workgroups per CU
-  const double mfma = 2.0 * e.bm * e.bn * e.bk / kFlopPerClk / e.efficiency;
+  const double eff = e.efficiency * (occupancy(c, id, epi) < e.occupancy ? kLowOccupancyRate : 1.0);
+  const double mfma = 2.0 * e.bm * e.bn * e.bk / kFlopPerClk / eff;
   const double load = (double)(e.bm + e.bn) * e.bk * 2.0 / kLoadBytesPerClk;
-  const double per_kt = std::max(share * std::max(mfma, load), kLatencyClk / (e.stages - 1));
-  const double store = share * 2.0 * e.bm * e.bn / kStoreBytesPerClk;
+  const double per_kt =
+      std::max(share * std::max(mfma, load), (e.pw ? kProducerLatencyClk : kLatencyClk) / (e.stages - 1));
+  const double store =
+      e.streamk ? share * 2.0 * e.bm * e.bn / kStoreBytesPerClk
+                : share * 2.0 * e.bm * e.bn / kTileStoreBytesPerClk * (epi == kEpiNone ? 1.0 : 2.0) *
+                      (occupancy(c, id, epi) >= 2 ? 0.5 : 1.0);
   const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk;
   double t = (double)cdiv(dp, grid) * (kts * per_kt + store);
   const int64_t st = tiles - dp;
@@ -186,9 +218,10 @@ double model_cost(const Context* c, const KernelEntry& e, int64_t M, int64_t N, 
   return std::max(t, hbm);
 }
 
-int64_t max_grid(const Context* c, const KernelEntry& e, int64_t M, int64_t N, int64_t K) {
+int64_t max_grid(const Context* c, int id, int epi, int64_t M, int64_t N, int64_t K) {
+  const KernelEntry& e = kKernels[id];
   const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
-  int64_t g = (int64_t)c->cus * e.occupancy;
+  int64_t g = (int64_t)c->cus * occupancy(c, id, epi);
   if (!e.streamk) return std::min(g, tiles);
   g = std::min(g, tiles * cdiv(K, e.bk));
   while (g > 1 && 2 * g * e.bm * e.bn * 4 > (int64_t)kWorkspaceBytes) --g;
@@ -200,7 +233,7 @@ int64_t max_grid(const Context* c, const KernelEntry& e, int64_t M, int64_t N, i
 // stream-K, the hybrid whose stream phase is the last partial round of
 // tiles, and the hybrid whose stream phase also takes one full round (more
 // iterations per workgroup, fewer owners per split tile).
-void consider(const Context* c, int id, int64_t M, int64_t N, int64_t K, int64_t grid, Plan* best) {
+void consider(const Context* c, int id, int epi, int64_t M, int64_t N, int64_t K, int64_t grid, Plan* best) {
   const KernelEntry& e = kKernels[id];
   const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
   int64_t cand[3] = {tiles, -1, -1};
@@ -215,7 +248,7 @@ void consider(const Context* c, int id, int64_t M, int64_t N, int64_t K, int64_t
   }
   for (int64_t dp : cand) {
     if (dp < 0 || (tiles - dp) * (e.threads / 64) > kCounterSlots) continue;
-    const double cost = model_cost(c, e, M, N, K, grid, dp);
+    const double cost = model_cost(c, id, epi, M, N, K, grid, dp);
     if (cost < best->cost * 0.999) {
       best->kernel = id, best->grid = grid, best->dp = dp, best->cost = cost;
     }
@@ -236,7 +269,7 @@ int64_t halo_rows(const KernelEntry& e, int64_t M, int halo) {
 
 // conv: only shapes with a conv epilogue (waves spanning every row), priced
 // on the rows their overlapping tile rows compute.
-Plan resolve(const Context* c, int64_t M0, int64_t N, int64_t K, bool head64 = false, bool conv = false) {
+Plan resolve(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bool head64 = false, bool conv = false) {
   Plan best;
   for (int id = 0; id < kNumKernels; ++id) {
     if (c->forced_kernel >= 0 && id != c->forced_kernel) continue;
@@ -253,15 +286,20 @@ Plan resolve(const Context* c, int64_t M0, int64_t N, int64_t K, bool head64 = f
       // shorter than M would stream the weight once per tile row.
       if (e.streamk && M > e.bm && (M <= 256 || cdiv(M, e.bm) * cdiv(N, e.bn) >= c->cus)) continue;
       if (!e.streamk && M <= 128) continue;
+      // LayerNorm epilogues on producer-wave shapes: measured slower in the
+      // ModernBERT chains than the plain 128x128 shape (the 128x128 one
+      // needs more registers than two workgroups per CU allow, the one-
+      // workgroup shapes have no second workgroup to hide the epilogue).
+      if (e.pw && epi_norm(epi) == kNormLayer) continue;
     }
-    const int64_t gmax = max_grid(c, e, M, N, K);
+    const int64_t gmax = max_grid(c, id, epi, M, N, K);
     if (c->forced_grid > 0) {
-      consider(c, id, M, N, K, std::min<int64_t>(c->forced_grid, gmax), &best);
+      consider(c, id, epi, M, N, K, std::min<int64_t>(c->forced_grid, gmax), &best);
       continue;
     }
     const int64_t gmin = e.streamk && M <= e.bm ? std::max<int64_t>(1, gmax / 4) : gmax;
     for (int64_t g = gmax; g >= gmin; g -= std::max<int64_t>(1, gmax / 16))
-      consider(c, id, M, N, K, g, &best);
+      consider(c, id, epi, M, N, K, g, &best);
   }
   return best;
 }
@@ -336,6 +374,16 @@ int sys1hip_init(int device, void** out) {
     return fail(SYS1HIP_EDEVICE, "sys1hip_init: device set-up failed (%s)", msg);
   }
   c->stream = c->own;
+  c->occ.assign((size_t)kNumKernels * kEpiCount, 0);
+  for (int id = 0; id < kNumKernels; ++id)
+    for (int epi = 0; epi < kEpiCount; ++epi) {
+      int n = 0;
+      const KernelFn fn = kKernels[id].fn[epi];
+      if (fn && hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn),
+                                                             kKernels[id].threads, 0) == hipSuccess)
+        c->occ[(size_t)id * kEpiCount + epi] = n;
+    }
+  (void)hipGetLastError();
   *out = c;
   return SYS1HIP_OK;
 }
@@ -400,7 +448,7 @@ int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epi
   const Context* c = static_cast<const Context*>(ctx);
   if (M <= 0 || N <= 0 || K <= 0)
     return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: bad shape");
-  const Plan p = resolve(c, M, N, K);
+  const Plan p = resolve(c, M, N, K, epi_id_from_flags(epilogue));
   const int id = p.kernel;
   if (name && cap > 0) {
     std::string s = kKernels[id].name;
@@ -450,7 +498,7 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
 
   int rc = use_device(c);
   if (rc) return rc;
-  const Plan p = resolve(c, M, N, K);
+  const Plan p = resolve(c, M, N, K, epi);
   const KernelEntry& e = kKernels[p.kernel];
   const int64_t grid = p.grid;
   if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
@@ -505,7 +553,7 @@ int sys1hip_linear_rope_qkv_bf16(void* ctx, const uint16_t* x, int64_t ldx, cons
   if (c->forced_kernel >= 0 && kKernels[c->forced_kernel].tn != 64)
     return fail(SYS1HIP_EINVAL, "sys1hip_linear_rope_qkv_bf16: forced kernel %s is not head-aligned",
                 kKernels[c->forced_kernel].name);
-  const Plan p = resolve(c, M, N, K, true);
+  const Plan p = resolve(c, M, N, K, kEpiRopeQkv, true);
   const KernelEntry& e = kKernels[p.kernel];
   if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
     return fail(SYS1HIP_ERANGE, "sys1hip_linear_rope_qkv_bf16: more split tiles than stream-K counters");
@@ -618,7 +666,7 @@ int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const ui
     return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: dimension above 2^30");
   int rc = use_device(c);
   if (rc) return rc;
-  const Plan p = resolve(c, M, N, K);
+  const Plan p = resolve(c, M, N, K, epi);
   const KernelEntry& e = kKernels[p.kernel];
   if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
     return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: more split tiles than stream-K counters");
@@ -693,7 +741,7 @@ int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx, con
   // shapes lose more in the GEMM than the fused form saves in traffic.
   const bool fused = c->forced_kernel >= 0 && kKernels[c->forced_kernel].wm == 1;
   const int epi = fused ? (norm ? kEpiNormRmsConvSilu : kEpiConvSilu) : (norm ? kEpiNormRms : kEpiNone);
-  const Plan p = resolve(c, M, N, K, false, fused);
+  const Plan p = resolve(c, M, N, K, epi, false, fused);
   const KernelEntry& e = kKernels[p.kernel];
   if (!e.fn[epi])
     return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: kernel %s has no conv epilogue", e.name);
