@@ -142,6 +142,7 @@ struct GemmArgs {
   int64_t ldx, ldw, ldr, ldy;
   int M, N, K, Nout;
   int dp_tiles;         // stream-K kernels: tiles run whole before the stream phase
+  int group_m;          // tile rows per raster group of the persistent schedule
   // kEpiRopeQkv: y holds planes q, k, v of [M, H] (H = Nout / 3, ld ldy),
   // `plane` elements apart; head_dim 64; cos/sin [positions, 32] f32;
   // pos[m] is token m's rotary position.

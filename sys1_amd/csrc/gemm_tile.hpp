@@ -140,7 +140,7 @@ struct Segment {
   int spos;       // stream-phase position of its first k-tile (st * kt_count + kt0)
 };
 
-// Persistent schedule over tiles rasterised in groups of kGroupM tile rows
+// Persistent schedule over tiles rasterised in groups of group_m tile rows
 // (tiles in flight together share x row panels and w column panels in L2).
 // The grid holds at most (CUs x resident workgroups per CU) workgroups G.
 //   Tile phase: tiles [0, dp_tiles), each a whole segment.  Workgroup b
@@ -164,11 +164,12 @@ struct TileWalk {
   int grid, sgrid, begin, end;  // sgrid: workgroups in the stream phase
   int dp_steps;
 
-  static constexpr int kGroupM = 4;
+  int group_m;
 
   // halo > 0: tile row tm covers rows [tm (BM - halo), + BM), so the halo
   // rows before each tile row's outputs are computed in the same tile.
-  __device__ TileWalk(int M, int N, int K, int BM, int BN, int BK, int dp, int halo = 0) {
+  __device__ TileWalk(int M, int N, int K, int BM, int BN, int BK, int dp, int group, int halo = 0) {
+    group_m = max(1, group);
     step_m = BM - halo;
     tiles_m = M <= BM ? 1 : 1 + (M - BM + step_m - 1) / step_m;
     tiles_n = (N + BN - 1) / BN;
@@ -201,10 +202,10 @@ struct TileWalk {
 
   // Tile index -> coordinates (grouped raster).
   __device__ void tile_coords(int t, int& tm, int& tn) const {
-    const int group = t / (kGroupM * tiles_n);
-    const int first_m = group * kGroupM;
-    const int gm = min(kGroupM, tiles_m - first_m);
-    const int in = t - group * kGroupM * tiles_n;
+    const int group = t / (group_m * tiles_n);
+    const int first_m = group * group_m;
+    const int gm = min(group_m, tiles_m - first_m);
+    const int in = t - group * group_m * tiles_n;
     tm = first_m + in % gm;
     tn = in / gm;
   }
@@ -266,7 +267,8 @@ __global__ __launch_bounds__((WM * WN + PW) * 64, OCC) void gemm_tile_kernel(Gem
   constexpr bool kConv = epi_base(EPI) == kEpiConvSilu;
   static_assert(!kConv || WM == 1, "conv epilogue: one wave row per tile");
   static_assert(PW == 0 || (!STREAMK && !kConv), "producer waves: plain tile schedule");
-  const TileWalk walk(a.M, a.N, a.K, BM, BN, BK, STREAMK ? a.dp_tiles : 1 << 30, kConv ? kConvHalo : 0);
+  const TileWalk walk(a.M, a.N, a.K, BM, BN, BK, STREAMK ? a.dp_tiles : 1 << 30, a.group_m,
+                      kConv ? kConvHalo : 0);
   if (walk.steps() == 0) return;
 
   const int tid = threadIdx.x;
