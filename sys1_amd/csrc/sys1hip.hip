@@ -166,7 +166,8 @@ constexpr double kHbmBytesPerClk = 1500.0;  // whole chip, sustained by a weight
 constexpr double kFixupClk = 2000.0;        // partial write + arrival
 constexpr double kLatencyClk = 1500.0;      // load issue -> data in LDS
 // With producer waves a refill is issued as soon as its stage is freed, not
-// behind the compute waves' MFMAs: a shorter effective latency.
+// behind the compute waves' MFMAs: a shorter effective latency (when every
+// CU runs at least one workgroup).
 constexpr double kProducerLatencyClk = 900.0;
 
 struct Plan {
@@ -196,8 +197,11 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
   const double eff = e.efficiency * (occupancy(c, id, epi) < e.occupancy ? kLowOccupancyRate : 1.0);
   const double mfma = 2.0 * e.bm * e.bn * e.bk / kFlopPerClk / eff;
   const double load = (double)(e.bm + e.bn) * e.bk * 2.0 / kLoadBytesPerClk;
-  const double per_kt =
-      std::max(share * std::max(mfma, load), (e.pw ? kProducerLatencyClk : kLatencyClk) / (e.stages - 1));
+  // (A grid below one workgroup per CU leaves each workgroup's load latency
+  // exposed: measured ~2200 cycles per k-tile for one 128x128 producer-wave
+  // workgroup per CU streaming a cold weight.)
+  const double latency = e.pw && grid >= c->cus ? kProducerLatencyClk : kLatencyClk;
+  const double per_kt = std::max(share * std::max(mfma, load), latency / (e.stages - 1));
   const double store =
       e.streamk ? share * 2.0 * e.bm * e.bn / kStoreBytesPerClk
                 : share * 2.0 * e.bm * e.bn / kTileStoreBytesPerClk * (epi == kEpiNone ? 1.0 : 2.0) *
