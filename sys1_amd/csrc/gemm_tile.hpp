@@ -259,7 +259,8 @@ struct TileWalk {
 // so a refill instruction that stalls issue while the load path drains
 // stalls no matrix work (tile schedule only).
 template <int BM, int BN, int WM, int WN, int STAGES, int BK_, int OCC, bool STREAMK, int EPI, int PW = 0>
-__global__ __launch_bounds__((WM * WN + PW) * 64, OCC) void gemm_tile_kernel(GemmArgs a) {
+__global__ __launch_bounds__((WM * WN + PW) * 64)
+__attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_tile_kernel(GemmArgs a) {
   using S = TileShape<BM, BN, WM, WN, STAGES, BK_>;
   constexpr int BK = S::BK;
   __shared__ __attribute__((aligned(1024))) char lds[S::kLdsBytes];
@@ -474,44 +475,52 @@ __global__ __launch_bounds__((WM * WN + PW) * 64, OCC) void gemm_tile_kernel(Gem
   // into w, c_n = sum_k of folded row n); then the base epilogue E runs.
   constexpr int E = epi_base(EPI);
   constexpr int NORM = epi_norm(EPI);
-  // All of a tile's row statistics and column sums are loaded before any of
+  // A tile's row statistics and column sums are all loaded before any of
   // them is used, so the epilogue waits for one round trip, not one per
   // block.
   auto normalize_tile = [&](int m0, int n0) {
-    float mu[S::FM], rs[S::FM];
+    float rs[S::FM];
 #pragma unroll
     for (int j = 0; j < S::FM; ++j) {
       const int m = min(m0 + wm * S::TM + j * 32 + frow, a.M - 1);
-      mu[j] = a.stats[2 * (int64_t)m];
       rs[j] = a.stats[2 * (int64_t)m + 1];
     }
-    f32x4 cs[S::FN][4];
     if constexpr (NORM == kNormLayer) {
+      // acc - mu_m c_n as one more MFMA per block: A holds c_n's bf16 split
+      // (hi, hi, lo) and B -mu_m's (hi, lo, hi) in k = 0..2 (lanes 0-31;
+      // zeros elsewhere), so the block gains c_hi mu_hi + c_hi mu_lo +
+      // c_lo mu_hi, each product exact in f32 (relative error ~2^-16 of
+      // mu c, the c_lo mu_lo term).  Two values per lane instead of the
+      // block's 16 column sums.
+      i32x4 ca[S::FN], mb[S::FM];
+#pragma unroll
+      for (int i = 0; i < S::FN; ++i) {
+        const float c = a.colsum[min(n0 + wn * S::TN + i * 32 + frow, a.N - 1)];
+        const __bf16 hi = to_bf16(c), lo = to_bf16(c - to_f32(hi));
+        bf16x8 v = {};
+        if (fk == 0) v[0] = hi, v[1] = hi, v[2] = lo;
+        ca[i] = __builtin_bit_cast(i32x4, v);
+      }
+#pragma unroll
+      for (int j = 0; j < S::FM; ++j) {
+        const int m = min(m0 + wm * S::TM + j * 32 + frow, a.M - 1);
+        const float nm = -a.stats[2 * (int64_t)m];
+        const __bf16 hi = to_bf16(nm), lo = to_bf16(nm - to_f32(hi));
+        bf16x8 v = {};
+        if (fk == 0) v[0] = hi, v[1] = lo, v[2] = hi;
+        mb[j] = __builtin_bit_cast(i32x4, v);
+      }
 #pragma unroll
       for (int i = 0; i < S::FN; ++i)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int n = n0 + wn * S::TN + i * 32 + 8 * g + 4 * fk;  // w row of register 4g + e: n + e
-          if (n + 3 < a.N) {
-            cs[i][g] = *reinterpret_cast<const f32x4*>(a.colsum + n);
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) cs[i][g][e] = a.colsum[min(n + e, a.N - 1)];
-          }
-        }
+        for (int j = 0; j < S::FM; ++j) acc[i][j] = mfma32(ca[i], mb[j], acc[i][j]);
     }
 #pragma unroll
     for (int i = 0; i < S::FN; ++i)
 #pragma unroll
       for (int j = 0; j < S::FM; ++j)
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float v = acc[i][j][4 * g + e];
-            if constexpr (NORM == kNormLayer) acc[i][j][4 * g + e] = rs[j] * (v - mu[j] * cs[i][g][e]);
-            else acc[i][j][4 * g + e] = v * rs[j];
-          }
+        for (int e = 0; e < 16; ++e) acc[i][j][e] *= rs[j];
   };
   // DeltaNet causal conv + SiLU over the in_proj qkv columns
   // (src/archs/qwen35_text.rs:515-526,632-650; src/kernels/qwen35.cu:3-29):

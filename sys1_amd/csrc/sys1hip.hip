@@ -290,11 +290,6 @@ Plan resolve(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bool h
       // shorter than M would stream the weight once per tile row.
       if (e.streamk && M > e.bm && (M <= 256 || cdiv(M, e.bm) * cdiv(N, e.bn) >= c->cus)) continue;
       if (!e.streamk && M <= 128) continue;
-      // LayerNorm epilogues on producer-wave shapes: measured slower in the
-      // ModernBERT chains than the plain 128x128 shape (the 128x128 one
-      // needs more registers than two workgroups per CU allow, the one-
-      // workgroup shapes have no second workgroup to hide the epilogue).
-      if (e.pw && epi_norm(epi) == kNormLayer) continue;
     }
     const int64_t gmax = max_grid(c, id, epi, M, N, K);
     if (c->forced_grid > 0) {
