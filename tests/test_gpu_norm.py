@@ -91,6 +91,31 @@ def test_norm_linear_matches_unfused_chain(dev, orc, kind, gated, M, N, K):
     print(f"[gpu]   rel_fro={rel:.2e} max_abs/max={mx:.2e}", flush=True)
 
 
+@pytest.mark.parametrize("offset", [4.0, 16.0])
+def test_layernorm_rows_with_large_means(dev, orc, offset):
+    """Rows whose mean is large against their spread: the epilogue's r (acc -
+    mu c) cancels heavily, and the -mu c term (a bf16 hi/lo-split MFMA in
+    the kernel) must keep the result within the projection tolerance, on the
+    producer-wave 128x128 shape and on the plain one."""
+    from sys1_amd import kernel_names
+    from sys1_amd.norm import NormLinear
+    M, N, K = 600, 2304, 768
+    x = orc.fill_normal((M, K), 61)
+    x += offset * (1.0 + orc.fill_normal((M, 1), 62, 0.25))
+    x = orc.round_bf16(x)
+    w, g = _weights(orc, N, K, 63, "layer")
+    ref = _ref(orc, x, w, g, "layer", 1e-5, None)
+    lin = NormLinear(to_gpu_bf16(w, torch), torch.from_numpy(g), "layer", 1e-5, None, device=dev)
+    try:
+        for name in ("tile_128x128_s2_w2x2_p4", "tile_128x128_s2_w2x2", None):
+            dev.set_kernel(kernel_names().index(name) if name else -1)
+            print(f"[gpu] layernorm offset={offset} kernel={name or 'auto'}", flush=True)
+            rel, mx = assert_parity(to_np(lin(to_gpu_bf16(x, torch))), ref, f"offset {offset} {name}")
+            print(f"[gpu]   rel_fro={rel:.2e} max_abs/max={mx:.2e}", flush=True)
+    finally:
+        dev.set_kernel(-1)
+
+
 def test_fold_is_exact_and_colsum_sums_the_folded_rows(dev, orc):
     from sys1_amd.norm import fold_norm_weight
     N, K = 300, 1032
