@@ -114,6 +114,7 @@ const KernelEntry kKernels[] = {
     tile_entry<256, 128, 2, 2, 3, 64, 1, false, 4>("tile_256x128_s3_w2x2_p4", 0.74f),
     tile_entry<128, 128, 2, 2, 2, 64, 2, false, 4>("tile_128x128_s2_w2x2_p4", 0.70f),
     tile_entry<128, 128, 2, 2, 2, 64, 2, false>("tile_128x128_s2_w2x2", 0.60f),
+    tile_entry<128, 96, 4, 1, 2, 64, 2, false, 4>("tile_128x96_s2_w4x1_p4", 0.53f),
     tile_entry<32, 256, 1, 4, 4, 64, 1, true>("stream_32x256_s4_w1x4", 0.50f),
     tile_entry<64, 256, 2, 4, 3, 64, 1, true>("stream_64x256_s3_w2x4", 0.60f),
     tile_entry<64, 256, 2, 4, 4, 64, 1, true>("stream_64x256_s4_w2x4", 0.60f),
@@ -193,7 +194,9 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
   const KernelEntry& e = kKernels[id];
   const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
   const int64_t kts = cdiv(K, e.bk);
-  const double share = std::max(1.0, (double)grid / c->cus);  // workgroups per CU
+  // Workgroups on the busiest CU: a grid between one and two per CU leaves
+  // some CUs running two, and those set the launch's time.
+  const double share = (double)std::max<int64_t>(1, cdiv(grid, c->cus));
   const double eff = e.efficiency * (occupancy(c, id, epi) < e.occupancy ? kLowOccupancyRate : 1.0);
   const double mfma = 2.0 * e.bm * e.bn * e.bk / kFlopPerClk / eff;
   const double load = (double)(e.bm + e.bn) * e.bk * 2.0 / kLoadBytesPerClk;
