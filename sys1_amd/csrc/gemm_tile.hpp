@@ -263,7 +263,19 @@ __global__ __launch_bounds__((WM * WN + PW) * 64)
 __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_tile_kernel(GemmArgs a) {
   using S = TileShape<BM, BN, WM, WN, STAGES, BK_>;
   constexpr int BK = S::BK;
-  __shared__ __attribute__((aligned(1024))) char lds[S::kLdsBytes];
+  // Residual epilogues of producer-wave tile kernels whose LDS budget has
+  // room: the producers copy each tile's residual block into LDS while its
+  // k-loop runs, so the epilogue does not wait on a read from HBM.
+  constexpr bool kResLds = PW > 0 && !STREAMK && epi_has_resid<epi_base(EPI)>() &&
+                           (S::kLdsBytes + BM * BN * 2) * OCC <= 160 * 1024 && (BM * BN * 2 / 1024) % PW == 0;
+  constexpr int kResBytes = kResLds ? BM * BN * 2 : 0;
+  __shared__ __attribute__((aligned(1024))) char lds[S::kLdsBytes + kResBytes];
+  char* const res_lds = lds + S::kLdsBytes;
+  // (every k-tile loop needs two k-steps per tile, so that a tile's copy,
+  // issued after its first barrier, lands before its last)
+  const bool res_in_lds = kResLds && a.K > BK_ && a.Nout >= 8 && a.Nout % 8 == 0 && a.ldr % 8 == 0 &&
+                          (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0 &&
+                          (int64_t)a.M * a.ldr * 2 < 0x7ffffff0ll;
 
   constexpr bool kConv = epi_base(EPI) == kEpiConvSilu;
   static_assert(!kConv || WM == 1, "conv epilogue: one wave row per tile");
@@ -363,14 +375,38 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
   if constexpr (PW > 0) {
     if (wave >= S::kWaves) {
       const int steps = walk.steps();
+      // The residual copy of tile `sg`: instruction i fills LDS bytes
+      // [1024 i, 1024 i + 1024) of the row-major [BM][BN] block.  Rows past
+      // M and columns past Nout read clamped (their outputs are not stored).
+      auto issue_res = [&](const Segment& sg) {
+        if constexpr (kResLds) {
+          const rsrc_t rr = make_rsrc_uniform(a.resid, 0x7ffffff0);
+          const int m0 = walk.row0(sg.tm), n0 = sg.tn * BN;
+#pragma unroll
+          for (int q = 0; q < BM * BN * 2 / 1024 / PW; ++q) {
+            const int i = q * PW + dwave;
+            const int e = i * 512 + lane * 8;
+            const int row = min(m0 + e / BN, a.M - 1), col = min(n0 + e % BN, a.Nout - 8);
+            dma16(rr, (unsigned)(((int64_t)row * a.ldr + col) * 2), (lds_void*)(res_lds + i * 1024));
+          }
+        }
+      };
+      Segment psg = walk.first_segment();  // the tile of step s
+      int pkt = psg.kt0;
       for (int t = 0; t < STAGES; ++t)
         if (t < steps) issue(t);
       if (steps >= STAGES) vm_wait<(STAGES - 1) * kDma>();
       else vm_wait<0>();
+      if (res_in_lds) issue_res(psg);
       __syncthreads();
       int stage = 0;
       for (int s = 0; s < steps; ++s) {
-        if (s + 1 < steps) {
+        // Before the barrier after which the tile's epilogue runs, its
+        // residual copy has landed too.
+        const bool tile_end = kResLds && pkt + 1 == psg.kt1;
+        if (res_in_lds && tile_end) {
+          vm_wait<0>();
+        } else if (s + 1 < steps) {
           if (s + STAGES - 1 < steps) vm_wait<(STAGES - 2) * kDma>();
           else vm_wait<0>();
         }
@@ -378,6 +414,17 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
         const int freed = stage;
         stage = stage + 1 == STAGES ? 0 : stage + 1;
         if (s + STAGES < steps) issue(freed);
+        // A tile's copy goes out after its first barrier: the compute waves
+        // have finished the previous tile's epilogue to get there.
+        if constexpr (kResLds) {
+          if (res_in_lds && s > 0 && pkt == psg.kt0) issue_res(psg);
+          if (tile_end && s + 1 < steps) {
+            psg = walk.next_segment(psg);
+            pkt = psg.kt0;
+          } else {
+            ++pkt;
+          }
+        }
       }
       vm_wait<0>();
       return;
@@ -737,7 +784,16 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
                 float b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
                 if constexpr (epi_has_bias<E>()) load8(a.bias + n, b, valid);
                 float r[8];
-                if constexpr (epi_has_resid<E>()) load8(a.resid + (int64_t)m * a.ldr + n, r, valid);
+                if constexpr (epi_has_resid<E>()) {
+                  if (kResLds && res_in_lds) {
+                    const bf16x8 rv = *reinterpret_cast<const bf16x8*>(
+                        res_lds + ((m - m0) * BN + (n - n0)) * 2);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) r[e] = to_f32(rv[e]);
+                  } else {
+                    load8(a.resid + (int64_t)m * a.ldr + n, r, valid);
+                  }
+                }
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                   float t = epi_pre<E>(to_f32(v[e]), b[e]);
