@@ -867,20 +867,28 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
     for (int g = g_lo; g <= g_hi; ++g) {
       // g's segment in this tile is its head iff g's range starts inside the tile.
       const unsigned src = slot_off(g, walk.start(g) >= tile_lo ? 0 : 1);
+      // All of one owner's loads are in flight together (these coherent
+      // reads come from beyond the L2: one round trip per owner, not one
+      // per block), then added in the same order as always.
+      f32x4 v[S::FN][S::FM][4];
 #pragma unroll
       for (int i = 0; i < S::FN; ++i)
 #pragma unroll
-        for (int j = 0; j < S::FM; ++j) {
+        for (int j = 0; j < S::FM; ++j)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f32x4 v = __builtin_bit_cast(
+          for (int q = 0; q < 4; ++q)
+            v[i][j][q] = __builtin_bit_cast(
                 f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                            wsr, (int)(src + ((i * S::FM + j) * 4 + q) * 64 * 16), 0, kCoherent));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[e];
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
+      for (int i = 0; i < S::FN; ++i)
+#pragma unroll
+        for (int j = 0; j < S::FM; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v[i][j][q][e];
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (lane == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
