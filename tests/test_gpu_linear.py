@@ -292,6 +292,32 @@ def test_tile_kernels_short_k_and_small_grids(dev, orc, kname):
         dev.set_kernel(-1)
 
 
+def test_residual_staged_in_lds_ragged_and_multi_tile(dev, orc):
+    """The 128x96 producer-wave kernel copies each tile's residual block into
+    LDS during the tile's k-loop.  Ragged N (the last tile's columns clamped),
+    N not a multiple of 8 and K within one k-tile (both read the residual
+    from HBM instead), and small grids (several tiles per workgroup, each
+    re-staging its block) must all match bf16(bf16(x.W) + r)."""
+    from sys1_amd import kernel_names
+    from sys1_amd.linear import Linear
+    dev.set_kernel(kernel_names().index("tile_128x96_s2_w4x1_p4"))
+    try:
+        for M, N, K in ((333, 776, 200), (333, 770, 200), (300, 384, 64), (700, 384, 328)):
+            x, w = _inputs(orc, M, N, K, 71 + N + K)
+            proj = orc.round_bf16(orc.linear_f64(orc.round_bf16(x), orc.round_bf16(w)).astype(np.float32))
+            res = orc.round_bf16(orc.fill_normal((M, N), 73))
+            ref = orc.round_bf16(proj + res)
+            lin = Linear(to_gpu_bf16(w, torch), device=dev)
+            xg, rg = to_gpu_bf16(x, torch), to_gpu_bf16(res, torch)
+            for g in (0, 1, 3, 7):
+                dev.set_grid(g)
+                print(f"[gpu] residual via LDS M={M} N={N} K={K} grid={g}", flush=True)
+                assert_parity(to_np(lin(xg, residual=rg)), ref, f"M={M} N={N} K={K} grid={g}")
+    finally:
+        dev.set_grid(0)
+        dev.set_kernel(-1)
+
+
 def test_python_errors(dev, orc):
     from sys1_amd import Sys1HipError
     from sys1_amd.linear import GatedLinear, Linear
