@@ -431,6 +431,16 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
     }
   }
 
+  // ---- fragment sets in registers (see the main loop):
+  //   kDeep: one set per k-step of a k-tile;  otherwise two (ping-pong);
+  //   kSingle: one, when two do not fit beside the accumulators in the
+  //     register budget (the other compute wave on the SIMD covers the LDS
+  //     latency that a single set exposes).
+  constexpr int kReads = S::FM + S::FN;  // LDS reads per fragment set
+  constexpr int kWavesPerSimd = ((S::kWaves + PW) * OCC + 3) / 4;  // register budget 512 / this
+  constexpr bool kDeep = S::KS == 4 && kReads * 4 * 4 <= 64 && kWavesPerSimd <= 3;
+  constexpr bool kSingle = !kDeep && S::FM * S::FN * 16 + 2 * kReads * 4 + 24 > 512 / kWavesPerSimd;
+
   // ---- fragment addressing (byte offsets within a stage): lane reads row
   // (base + lane%32) of chunk 2*ks + lane/32.
   const int frow = lane & 31;
@@ -449,12 +459,35 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
     wrow_swz[i] = lds_swz<BK>(r);
   }
 
+  // kSingle: chunk 2 ks + fk of a row sits at ((fk ^ swz) << 4) ^ (ks << 5),
+  // so one base register per fragment row serves every k-step; the bases
+  // are redefined (opaquely) each k-tile, so the compiler cannot hoist one
+  // address per k-step out of the loop (which spills at this budget).
+  int xaddr[S::FM], waddr[S::FN];
+#pragma unroll
+  for (int j = 0; j < S::FM; ++j) xaddr[j] = xrow_off[j] + ((fk ^ xrow_swz[j]) << 4);
+#pragma unroll
+  for (int i = 0; i < S::FN; ++i) waddr[i] = wrow_off[i] + ((fk ^ wrow_swz[i]) << 4);
+  auto refresh_addr = [&]() {
+#pragma unroll
+    for (int j = 0; j < S::FM; ++j) asm volatile("" : "+v"(xaddr[j]));
+#pragma unroll
+    for (int i = 0; i < S::FN; ++i) asm volatile("" : "+v"(waddr[i]));
+  };
+
   struct Frags {
     i32x4 x[S::FM];
     i32x4 w[S::FN];
   };
   auto read = [&](Frags& f, int stage, int ks) {
     const char* base = lds + stage * S::kStageBytes;
+    if constexpr (kSingle) {
+#pragma unroll
+      for (int j = 0; j < S::FM; ++j) f.x[j] = *reinterpret_cast<const i32x4*>(base + (xaddr[j] ^ (ks << 5)));
+#pragma unroll
+      for (int i = 0; i < S::FN; ++i) f.w[i] = *reinterpret_cast<const i32x4*>(base + (waddr[i] ^ (ks << 5)));
+      return;
+    }
     const int c = ks * 2 + fk;
 #pragma unroll
     for (int j = 0; j < S::FM; ++j)
@@ -915,18 +948,16 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
 
   Segment csg = walk.first_segment();  // compute cursor
   int ckt = csg.kt0;
-  // Two schedules of a k-tile's KS k-steps of MFMAs (fragment reads one
-  // k-step ahead of their MFMAs in both):
+  // Schedules of a k-tile's KS k-steps of MFMAs (fragment reads one k-step
+  // ahead of their MFMAs in the first two; kSingle reads each k-step's set
+  // behind the previous k-step's MFMAs and waits for it):
   //   kDeep (one fragment set per k-step, when they fit in registers): the
   //     barrier that frees the stage comes after the k-tile's last two
   //     fragment sets are in registers, so two k-steps of MFMAs run after it,
   //     covering the next stage's first fragment reads, with the freed
   //     stage's refill issued between them;
   //   otherwise (ping-pong sets): one k-step of MFMAs after the barrier.
-  constexpr int kReads = S::FM + S::FN;  // LDS reads per fragment set
-  constexpr int kWavesPerSimd = ((S::kWaves + PW) * OCC + 3) / 4;  // register budget 512 / this
-  constexpr bool kDeep = S::KS == 4 && kReads * 4 * 4 <= 64 && kWavesPerSimd <= 3;
-  constexpr int kSets = kDeep ? 4 : 2;
+  constexpr int kSets = kDeep ? 4 : kSingle ? 1 : 2;
   Frags fr[kSets];
   if (steps > 0) {
     read(fr[0], 0, 0);
@@ -934,6 +965,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
   }
   int stage = 0;
   for (int s = 0; s < steps; ++s) {
+    if constexpr (kSingle) refresh_addr();
     if constexpr (kDeep) {
       // fr[0] (and fr[1], one set later) of this k-tile were read after the
       // previous barrier.  Waiting for them explicitly keeps the compiler
@@ -949,6 +981,17 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
       __builtin_amdgcn_sched_barrier(0);
       mma(fr[1]);
       __builtin_amdgcn_sched_barrier(0);
+    } else if constexpr (kSingle) {
+      // Each k-step's fragments are waited for just before its MFMAs.
+#pragma unroll
+      for (int ks = 0; ks < S::KS; ++ks) {
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        __builtin_amdgcn_sched_barrier(0);
+        mma(fr[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + 1 < S::KS) read(fr[0], stage, ks + 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     } else {
       // As above: the k-tile's first fragments are in.
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt unconstrained
@@ -983,7 +1026,11 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
 #pragma unroll
       for (int i = 0; i < kDma; ++i) if constexpr (kIssue) dma_one(r, i);
     };
-    if constexpr (kDeep && kSpread) {
+    if constexpr (kSingle) {
+      if (s + 1 < steps) read(fr[0], stage, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      refill_all();
+    } else if constexpr (kDeep && kSpread) {
       constexpr int kHalf = kDma / 2;
       if (s + 1 < steps) {
         read(fr[0], stage, 0);

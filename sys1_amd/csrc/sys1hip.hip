@@ -74,6 +74,7 @@ struct KernelEntry {
   int tn;               // output columns per wave (the RoPE epilogue needs 64: one head)
   int wm;               // waves along M (the conv epilogue needs 1: a wave holds every row)
   int pw;               // producer waves (0: the compute waves issue the refills)
+  float swiglu_efficiency;  // efficiency with a SwiGLU epilogue, when it differs (0: the same)
   KernelFn fn[kEpiCount];
 };
 
@@ -86,8 +87,8 @@ constexpr KernelFn conv_fn() {
 
 // PW: producer waves (see gemm_tile_kernel).
 template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK, int PW = 0>
-constexpr KernelEntry tile_entry(const char* name, float eff) {
-  return KernelEntry{name, BM, BN, (WM * WN + PW) * 64, OCC, SK, eff, BK, ST, BN / WN, WM, PW,
+constexpr KernelEntry tile_entry(const char* name, float eff, float swiglu_eff = 0.0f) {
+  return KernelEntry{name, BM, BN, (WM * WN + PW) * 64, OCC, SK, eff, BK, ST, BN / WN, WM, PW, swiglu_eff,
                      {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 0, PW>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 1, PW>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 2, PW>,
@@ -110,6 +111,10 @@ constexpr KernelEntry tile_entry(const char* name, float eff) {
 const KernelEntry kKernels[] = {
     // Large M.  _p4: four producer waves issue the refills (see gemm_tile_kernel).
     tile_entry<256, 256, 2, 4, 2, 64, 1, false>("tile_256x256_s2_w2x4", 0.80f),
+    // (one fragment set: measured ~10% slower than the plain 256x256 except
+    // with the SwiGLU epilogues, where it is ~10% faster; with GeGLU's erf it
+    // spills and runs at half speed)
+    tile_entry<256, 256, 2, 4, 2, 64, 1, false, 4>("tile_256x256_s2_w2x4_p4", 0.70f, 0.88f),
     tile_entry<128, 256, 2, 4, 3, 64, 1, false, 4>("tile_128x256_s3_w2x4_p4", 0.50f),
     tile_entry<256, 128, 2, 2, 3, 64, 1, false, 4>("tile_256x128_s3_w2x2_p4", 0.74f),
     tile_entry<128, 128, 2, 2, 2, 64, 2, false, 4>("tile_128x128_s2_w2x2_p4", 0.70f),
@@ -197,7 +202,9 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
   // Workgroups on the busiest CU: a grid between one and two per CU leaves
   // some CUs running two, and those set the launch's time.
   const double share = (double)std::max<int64_t>(1, cdiv(grid, c->cus));
-  const double eff = e.efficiency * (occupancy(c, id, epi) < e.occupancy ? kLowOccupancyRate : 1.0);
+  const double base_eff =
+      epi_base(epi) == kEpiSwiglu && e.swiglu_efficiency > 0.0f ? e.swiglu_efficiency : e.efficiency;
+  const double eff = base_eff * (occupancy(c, id, epi) < e.occupancy ? kLowOccupancyRate : 1.0);
   const double mfma = 2.0 * e.bm * e.bn * e.bk / kFlopPerClk / eff;
   const double load = (double)(e.bm + e.bn) * e.bk * 2.0 / kLoadBytesPerClk;
   // (A grid below one workgroup per CU leaves each workgroup's load latency
