@@ -70,11 +70,34 @@ __device__ __forceinline__ __bf16 to_bf16(float v) { return static_cast<__bf16>(
 __device__ __forceinline__ float to_f32(__bf16 v) { return static_cast<float>(v); }
 __device__ __forceinline__ float round_bf16(float v) { return to_f32(to_bf16(v)); }
 
+// erfc(x) for x >= 0 with fractional error below 1.2e-7: the Chebyshev fit
+// "erfcc" of W. H. Press et al., Numerical Recipes in C, 2nd ed., section
+// 6.2: erfc(x) = t exp(-x^2 + P(t)), t = 1 / (1 + x / 2), P of degree 9.
+// Branch-free; the reciprocal and exponential are the hardware ones.
+__device__ __forceinline__ float erfc_nr(float x) {
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, x, 1.0f));
+  float p = 0.17087277f;
+  p = fmaf(p, t, -0.82215223f);
+  p = fmaf(p, t, 1.48851587f);
+  p = fmaf(p, t, -1.13520398f);
+  p = fmaf(p, t, 0.27886807f);
+  p = fmaf(p, t, -0.18628806f);
+  p = fmaf(p, t, 0.09678418f);
+  p = fmaf(p, t, 0.37409196f);
+  p = fmaf(p, t, 1.00002368f);
+  return t * __expf(fmaf(p, t, -1.26551223f) - x * x);
+}
+
 // Exact (erf) GELU: 0.5 v (1 + erf(v / sqrt 2)), the activation of the
 // reference's GeGLU (src/kernels/modernbert.cu:9-14 writes it as v * Phi(v))
-// and of candle's gelu_erf.  erff is ROCm's device-library erf.
+// and of candle's gelu_erf, in the reference's f32 sequence: erf is formed
+// as 1 - erfc or erfc - 1, then 1 + erf is rounded as the reference rounds
+// it.  Over every finite bf16 input this gives the bf16 result of the same
+// sequence with a correctly rounded f32 erf.
 __device__ __forceinline__ float gelu_erf(float v) {
-  return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f));
+  const float e = erfc_nr(fabsf(v) * 0.70710678118654752f);
+  const float erf = v >= 0.0f ? 1.0f - e : e - 1.0f;
+  return 0.5f * v * (1.0f + erf);
 }
 
 // SiLU: v / (1 + e^-v) (src/archs/qwen35_text.rs:239).

@@ -318,6 +318,38 @@ def test_residual_staged_in_lds_ragged_and_multi_tile(dev, orc):
         dev.set_kernel(-1)
 
 
+def test_gelu_every_bf16_input(dev, orc):
+    """The GeGLU epilogue's GELU over every finite bf16 gate value (the gate is
+    the bf16-rounded projection, so these are all the inputs it can see),
+    against the reference's f32 sequence 0.5 v (1 + erf(v / sqrt 2)) with a
+    correctly rounded f32 erf, each result rounded to bf16: a projection with
+    an identity gate block and an up block that reads a column of ones makes
+    the output exactly bf16(gelu(v)).  At most 0.1% may differ, by one bf16
+    ulp (the hardware exponential and reciprocal inside erfc)."""
+    import math
+    from sys1_amd.linear import GatedLinear
+    bits = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    v = bits[np.isfinite(bits)]
+    v = np.concatenate([v, np.zeros((-v.size) % 64, np.float32)])
+    M = v.size // 64
+    x = np.zeros((M, 128), np.float32)
+    x[:, :64] = v.reshape(M, 64)
+    x[:, 64] = 1.0
+    gate = np.zeros((64, 128), np.float32)
+    gate[:, :64] = np.eye(64, dtype=np.float32)
+    up = np.zeros((64, 128), np.float32)
+    up[:, 64] = 1.0
+    lin = GatedLinear(gate=to_gpu_bf16(gate, torch), up=to_gpu_bf16(up, torch), activation="gelu", device=dev)
+    print(f"[gpu] gelu over {v.size} bf16 values", flush=True)
+    y = to_np(lin(to_gpu_bf16(x, torch))).reshape(-1)
+    erf32 = np.array([math.erf(float(a) / math.sqrt(2.0)) for a in v], np.float64).astype(np.float32)
+    ref = orc.round_bf16((np.float32(0.5) * v * (np.float32(1.0) + erf32)).astype(np.float32))
+    diff = (y != ref) & ~((y == 0) & (ref == 0))
+    assert diff.mean() <= 1e-3, f"{int(diff.sum())} of {v.size} differ"
+    if diff.any():
+        assert (np.abs(y[diff] - ref[diff]) <= bf16_ulp(ref[diff]) + 1e-30).all()
+
+
 def test_python_errors(dev, orc):
     from sys1_amd import Sys1HipError
     from sys1_amd.linear import GatedLinear, Linear
