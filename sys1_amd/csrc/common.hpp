@@ -100,8 +100,11 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return 0.5f * v * (1.0f + erf);
 }
 
-// SiLU: v / (1 + e^-v) (src/archs/qwen35_text.rs:239).
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+// SiLU: v / (1 + e^-v) (src/archs/qwen35_text.rs:239), with the hardware
+// exponential and reciprocal (the IEEE division costs ~6% of a gated
+// projection); its bf16 results match the correctly rounded f32 sequence on
+// all but a few of the bf16 inputs, by one ulp.
+__device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
 // One output element of the non-gated epilogues from the f32 accumulator.
 // Rounding mirrors the unfused reference: projection -> bf16, then each op

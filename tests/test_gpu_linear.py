@@ -345,6 +345,40 @@ def test_gelu_every_bf16_input(dev, orc):
     erf32 = np.array([math.erf(float(a) / math.sqrt(2.0)) for a in v], np.float64).astype(np.float32)
     ref = orc.round_bf16((np.float32(0.5) * v * (np.float32(1.0) + erf32)).astype(np.float32))
     diff = (y != ref) & ~((y == 0) & (ref == 0))
+    print(f"[gpu]   {int(diff.sum())} of {v.size} differ", flush=True)
+    assert diff.mean() <= 1e-3, f"{int(diff.sum())} of {v.size} differ"
+    if diff.any():
+        assert (np.abs(y[diff] - ref[diff]) <= bf16_ulp(ref[diff]) + 1e-30).all()
+
+
+def test_silu_every_bf16_input(dev, orc):
+    """The SwiGLU epilogue's SiLU over every finite bf16 gate value, against
+    the f32 sequence v / (1 + exp(-v)) with a correctly rounded exp and
+    division, rounded to bf16 (the same identity-gate construction as the
+    GELU test).  At most 0.1% may differ, by one bf16 ulp (the hardware
+    exponential and reciprocal)."""
+    import math
+    from sys1_amd.linear import GatedLinear
+    bits = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    v = bits[np.isfinite(bits)]
+    v = np.concatenate([v, np.zeros((-v.size) % 64, np.float32)])
+    M = v.size // 64
+    x = np.zeros((M, 128), np.float32)
+    x[:, :64] = v.reshape(M, 64)
+    x[:, 64] = 1.0
+    gate = np.zeros((64, 128), np.float32)
+    gate[:, :64] = np.eye(64, dtype=np.float32)
+    up = np.zeros((64, 128), np.float32)
+    up[:, 64] = 1.0
+    lin = GatedLinear(gate=to_gpu_bf16(gate, torch), up=to_gpu_bf16(up, torch), activation="silu", device=dev)
+    print(f"[gpu] silu over {v.size} bf16 values", flush=True)
+    y = to_np(lin(to_gpu_bf16(x, torch))).reshape(-1)
+    with np.errstate(over="ignore"):
+        e32 = np.array([math.exp(min(-float(a), 700.0)) for a in v], np.float64).astype(np.float32)
+        den = (np.float32(1.0) + e32).astype(np.float32)
+        ref = orc.round_bf16((v.astype(np.float64) / den.astype(np.float64)).astype(np.float32))
+    diff = (y != ref) & ~((y == 0) & (ref == 0))
+    print(f"[gpu]   {int(diff.sum())} of {v.size} differ", flush=True)
     assert diff.mean() <= 1e-3, f"{int(diff.sum())} of {v.size} differ"
     if diff.any():
         assert (np.abs(y[diff] - ref[diff]) <= bf16_ulp(ref[diff]) + 1e-30).all()
