@@ -120,6 +120,7 @@ const KernelEntry kKernels[] = {
     tile_entry<128, 128, 2, 2, 2, 64, 2, false, 4>("tile_128x128_s2_w2x2_p4", 0.70f),
     tile_entry<128, 128, 2, 2, 2, 64, 2, false>("tile_128x128_s2_w2x2", 0.60f),
     tile_entry<128, 96, 4, 1, 2, 64, 2, false, 4>("tile_128x96_s2_w4x1_p4", 0.53f),
+    tile_entry<128, 192, 4, 2, 3, 64, 1, false, 4>("tile_128x192_s3_w4x2_p4", 0.60f),
     tile_entry<32, 256, 1, 4, 4, 64, 1, true>("stream_32x256_s4_w1x4", 0.50f),
     tile_entry<64, 256, 2, 4, 3, 64, 1, true>("stream_64x256_s3_w2x4", 0.60f),
     tile_entry<64, 256, 2, 4, 4, 64, 1, true>("stream_64x256_s4_w2x4", 0.60f),
