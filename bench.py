@@ -261,7 +261,7 @@ def main():
         torch.cuda.synchronize()
         for p, M, e0, e1 in recs:
             d = per_proj.setdefault(p.name, {"n": 0, "ms": 0.0, "flop": 0, "bytes": 0,
-                                             "K": p.K, "N": p.N})
+                                             "K": p.K, "N": p.N, "epi": p.epi})
             d["n"] += 1
             d["ms"] += e0.elapsed_time(e1)
             d["flop"] += p.flops(M)
@@ -272,7 +272,7 @@ def main():
         flop_per = d["flop"] / d["n"]
         byte_per = d["bytes"] / d["n"]
         ai = flop_per / byte_per
-        kid, kname = dev.query_kernel(int(np.mean(Ms)), d["N"], d["K"], 0)
+        kid, kname = dev.query_kernel(int(np.mean(Ms)), d["N"], d["K"], d["epi"])
         if ai >= RIDGE:
             achieved = flop_per / avg_s / 1e12
             roofline = {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
