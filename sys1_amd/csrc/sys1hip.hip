@@ -75,6 +75,7 @@ struct KernelEntry {
   int wm;               // waves along M (the conv epilogue needs 1: a wave holds every row)
   int pw;               // producer waves (0: the compute waves issue the refills)
   float swiglu_efficiency;  // efficiency with a SwiGLU epilogue, when it differs (0: the same)
+  float long_k_efficiency;  // efficiency for K > kLongK, when it differs (0: the same)
   KernelFn fn[kEpiCount];
 };
 
@@ -87,8 +88,8 @@ constexpr KernelFn conv_fn() {
 
 // PW: producer waves (see gemm_tile_kernel).
 template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK, int PW = 0>
-constexpr KernelEntry tile_entry(const char* name, float eff, float swiglu_eff = 0.0f) {
-  return KernelEntry{name, BM, BN, (WM * WN + PW) * 64, OCC, SK, eff, BK, ST, BN / WN, WM, PW, swiglu_eff,
+constexpr KernelEntry tile_entry(const char* name, float eff, float swiglu_eff = 0.0f, float long_k_eff = 0.0f) {
+  return KernelEntry{name, BM, BN, (WM * WN + PW) * 64, OCC, SK, eff, BK, ST, BN / WN, WM, PW, swiglu_eff, long_k_eff,
                      {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 0, PW>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 1, PW>,
                       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 2, PW>,
@@ -121,6 +122,9 @@ const KernelEntry kKernels[] = {
     tile_entry<128, 128, 2, 2, 2, 64, 2, false>("tile_128x128_s2_w2x2", 0.60f),
     tile_entry<128, 96, 4, 1, 2, 64, 2, false, 4>("tile_128x96_s2_w4x1_p4", 0.53f),
     tile_entry<128, 192, 4, 2, 3, 64, 1, false, 4>("tile_128x192_s3_w4x2_p4", 0.60f),
+    // (two stages only: with K beyond a few thousand its panels stream from
+    // beyond the L2 and the one k-tile in flight exposes the latency)
+    tile_entry<256, 192, 4, 2, 2, 64, 1, false, 4>("tile_256x192_s2_w4x2_p4", 0.80f, 0.0f, 0.60f),
     tile_entry<32, 256, 1, 4, 4, 64, 1, true>("stream_32x256_s4_w1x4", 0.50f),
     tile_entry<64, 256, 2, 4, 3, 64, 1, true>("stream_64x256_s3_w2x4", 0.60f),
     tile_entry<64, 256, 2, 4, 4, 64, 1, true>("stream_64x256_s4_w2x4", 0.60f),
@@ -172,6 +176,7 @@ constexpr double kTileStoreBytesPerClk = 32.0;
 constexpr double kHbmBytesPerClk = 1500.0;  // whole chip, sustained by a weight stream
 constexpr double kFixupClk = 2000.0;        // partial write + arrival
 constexpr double kLatencyClk = 1500.0;      // load issue -> data in LDS
+constexpr int64_t kLongK = 4096;            // see KernelEntry::long_k_efficiency
 // With producer waves a refill is issued as soon as its stage is freed, not
 // behind the compute waves' MFMAs: a shorter effective latency (when every
 // CU runs at least one workgroup).
@@ -203,8 +208,9 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
   // Workgroups on the busiest CU: a grid between one and two per CU leaves
   // some CUs running two, and those set the launch's time.
   const double share = (double)std::max<int64_t>(1, cdiv(grid, c->cus));
-  const double base_eff =
+  double base_eff =
       epi_base(epi) == kEpiSwiglu && e.swiglu_efficiency > 0.0f ? e.swiglu_efficiency : e.efficiency;
+  if (K > kLongK && e.long_k_efficiency > 0.0f) base_eff = e.long_k_efficiency;
   const double eff = base_eff * (occupancy(c, id, epi) < e.occupancy ? kLowOccupancyRate : 1.0);
   const double mfma = 2.0 * e.bm * e.bn * e.bk / kFlopPerClk / eff;
   const double load = (double)(e.bm + e.bn) * e.bk * 2.0 / kLoadBytesPerClk;
