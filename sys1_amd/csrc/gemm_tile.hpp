@@ -125,7 +125,6 @@ struct TileShape {
   static constexpr int kDma = DT / kWaves;           // per wave per k-tile
   static_assert(TM % 32 == 0 && TN % 32 == 0, "wave tile must be whole 32x32 blocks");
   static_assert(BM % RPI == 0 && BN % RPI == 0, "whole DMA instructions per tile");
-  static_assert(DT % kWaves == 0, "DMA instructions deal evenly over the waves");
   static_assert(STAGES >= 2, "at least double buffering");
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget of one gfx950 CU");
   static_assert(kDma * (STAGES - 1) < 64, "vmcnt field");
@@ -305,7 +304,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
   // K-tail test runs on a tile's last, partial k-tile only.
   constexpr int kDW = PW ? PW : S::kWaves;  // waves that issue refills
   constexpr int kDma = S::DT / kDW;          // refill instructions per issuing wave per k-tile
-  static_assert(S::XT % kDW == 0 && S::DT % kDW == 0, "x and w instructions split evenly per wave");
+  static_assert(S::XT % kDW == 0 && S::DT % kDW == 0, "x and w instructions deal evenly over the waves");
   static_assert(kDma * (STAGES - 1) < 64, "vmcnt field");
   constexpr int kXDma = S::XT / kDW;
   const int dwave = PW ? wave - S::kWaves : wave;

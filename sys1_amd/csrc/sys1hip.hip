@@ -125,6 +125,7 @@ const KernelEntry kKernels[] = {
     // (two stages only: with K beyond a few thousand its panels stream from
     // beyond the L2 and the one k-tile in flight exposes the latency)
     tile_entry<256, 192, 4, 2, 2, 64, 1, false, 4>("tile_256x192_s2_w4x2_p4", 0.80f, 0.0f, 0.60f),
+    tile_entry<256, 160, 8, 1, 3, 64, 1, false, 4>("tile_256x160_s3_w8x1_p4", 0.80f),
     tile_entry<32, 256, 1, 4, 4, 64, 1, true>("stream_32x256_s4_w1x4", 0.50f),
     tile_entry<64, 256, 2, 4, 3, 64, 1, true>("stream_64x256_s3_w2x4", 0.60f),
     tile_entry<64, 256, 2, 4, 4, 64, 1, true>("stream_64x256_s4_w2x4", 0.60f),
