@@ -292,17 +292,20 @@ def test_tile_kernels_short_k_and_small_grids(dev, orc, kname):
         dev.set_kernel(-1)
 
 
-def test_residual_staged_in_lds_ragged_and_multi_tile(dev, orc):
+@pytest.mark.parametrize("kname", ["tile_128x96_s2_w4x1_p4", "tile_128x192_s3_w4x2_p4"])
+def test_residual_staged_in_lds_ragged_and_multi_tile(dev, orc, kname):
     """The 128x96 producer-wave kernel copies each tile's residual block into
-    LDS during the tile's k-loop.  Ragged N (the last tile's columns clamped),
-    N not a multiple of 8 and K within one k-tile (both read the residual
-    from HBM instead), and small grids (several tiles per workgroup, each
-    re-staging its block) must all match bf16(bf16(x.W) + r)."""
+    LDS during the tile's k-loop; the 128x192 one, the other residual shape,
+    reads it from HBM in the epilogue.  Ragged N (the last tile's columns
+    clamped), N not a multiple of 8 and K within one k-tile (both read the
+    residual from HBM on the 128x96 kernel too), K of two k-tiles, and small
+    grids (several tiles per workgroup, each re-staging its block) must all
+    match bf16(bf16(x.W) + r)."""
     from sys1_amd import kernel_names
     from sys1_amd.linear import Linear
-    dev.set_kernel(kernel_names().index("tile_128x96_s2_w4x1_p4"))
+    dev.set_kernel(kernel_names().index(kname))
     try:
-        for M, N, K in ((333, 776, 200), (333, 770, 200), (300, 384, 64), (700, 384, 328)):
+        for M, N, K in ((333, 776, 200), (333, 770, 200), (300, 384, 64), (300, 384, 128), (700, 384, 328)):
             x, w = _inputs(orc, M, N, K, 71 + N + K)
             proj = orc.round_bf16(orc.linear_f64(orc.round_bf16(x), orc.round_bf16(w)).astype(np.float32))
             res = orc.round_bf16(orc.fill_normal((M, N), 73))
@@ -311,7 +314,7 @@ def test_residual_staged_in_lds_ragged_and_multi_tile(dev, orc):
             xg, rg = to_gpu_bf16(x, torch), to_gpu_bf16(res, torch)
             for g in (0, 1, 3, 7):
                 dev.set_grid(g)
-                print(f"[gpu] residual via LDS M={M} N={N} K={K} grid={g}", flush=True)
+                print(f"[gpu] {kname} residual M={M} N={N} K={K} grid={g}", flush=True)
                 assert_parity(to_np(lin(xg, residual=rg)), ref, f"M={M} N={N} K={K} grid={g}")
     finally:
         dev.set_grid(0)
