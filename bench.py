@@ -245,11 +245,14 @@ def main():
 
     # Roofline pass: same steps, HIP events around every launch, grouped by
     # projection kind (each kind is one kernel instantiation per shape).
+    # Each step's launches queue behind a spin kernel that outlasts the
+    # host's enqueue of that step, so the GPU runs behind the host and the
+    # events around a launch bracket the kernel, not the host call (small-M
+    # kernels are shorter than one call's host time).
     roofline = None
     per_proj = {}
     if not args.no_roofline:
-        recs = []
-        for s in range(args.steps):
+        def enqueue_events(s, recs):
             for p, fn, a in prepared[s % len(Ms)]:
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
@@ -258,6 +261,21 @@ def main():
                 if rc:
                     raise RuntimeError(f"launch failed: {rc}")
                 recs.append((p, Ms[s % len(Ms)], e0, e1))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        enqueue_events(0, [])
+        host_s = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record()
+        torch.cuda._sleep(1 << 20)
+        c1.record()
+        torch.cuda.synchronize()
+        spin_cycles = int((1 << 20) * 2.0 * host_s / (c0.elapsed_time(c1) * 1e-3)) + 1
+        recs = []
+        for s in range(args.steps):
+            torch.cuda._sleep(spin_cycles)
+            enqueue_events(s, recs)
         torch.cuda.synchronize()
         for p, M, e0, e1 in recs:
             d = per_proj.setdefault(p.name, {"n": 0, "ms": 0.0, "flop": 0, "bytes": 0,

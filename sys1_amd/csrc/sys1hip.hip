@@ -8,7 +8,9 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "common.hpp"
@@ -44,6 +46,32 @@ int fail(int code, const char* fmt, ...) {
     if (e_ != hipSuccess) return fail(SYS1HIP_EDEVICE, "%s: %s", #expr, hipGetErrorString(e_)); \
   } while (0)
 
+struct Plan {
+  int kernel = 0;
+  int64_t grid = 1;
+  int64_t dp = 0;  // tiles run whole before the stream phase (stream-K kernels)
+  double cost = 1e300;
+};
+
+struct PlanKey {
+  int64_t M, N, K;
+  int epi;
+  bool head64, conv;
+  bool operator==(const PlanKey& o) const {
+    return M == o.M && N == o.N && K == o.K && epi == o.epi && head64 == o.head64 && conv == o.conv;
+  }
+};
+
+struct PlanKeyHash {
+  size_t operator()(const PlanKey& k) const {
+    uint64_t h = (uint64_t)k.M * 0x9E3779B97F4A7C15ull;
+    h ^= ((uint64_t)k.N * 0xC2B2AE3D27D4EB4Full) + (h << 6) + (h >> 2);
+    h ^= ((uint64_t)k.K * 0x165667B19E3779F9ull) + (h << 6) + (h >> 2);
+    h ^= (uint64_t)(k.epi * 4 + k.head64 * 2 + k.conv) + (h << 6) + (h >> 2);
+    return (size_t)h;
+  }
+};
+
 struct Context {
   int device = 0;
   hipStream_t own = nullptr;
@@ -58,6 +86,11 @@ struct Context {
   // Resident workgroups per CU of each (kernel, epilogue) as the runtime
   // reports them (an epilogue that needs more registers can fit fewer).
   std::vector<int> occ;
+  // Chosen plans of unforced calls, keyed by shape and epilogue: pricing
+  // every (kernel, grid) takes several microseconds of host time, more than
+  // a small-M projection's kernel.
+  std::mutex plan_mu;
+  std::unordered_map<PlanKey, Plan, PlanKeyHash> plans;
 };
 
 using KernelFn = void (*)(GemmArgs);
@@ -183,13 +216,6 @@ constexpr int64_t kLongK = 4096;            // see KernelEntry::long_k_efficienc
 // CU runs at least one workgroup).
 constexpr double kProducerLatencyClk = 900.0;
 
-struct Plan {
-  int kernel = 0;
-  int64_t grid = 1;
-  int64_t dp = 0;  // tiles run whole before the stream phase (stream-K kernels)
-  double cost = 1e300;
-};
-
 int occupancy(const Context* c, int id, int epi) {
   const int n = c->occ.empty() ? 0 : c->occ[(size_t)id * kEpiCount + epi];
   return n > 0 ? std::min(n, kKernels[id].occupancy) : kKernels[id].occupancy;
@@ -291,7 +317,7 @@ int64_t halo_rows(const KernelEntry& e, int64_t M, int halo) {
 
 // conv: only shapes with a conv epilogue (waves spanning every row), priced
 // on the rows their overlapping tile rows compute.
-Plan resolve(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bool head64 = false, bool conv = false) {
+Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bool head64, bool conv) {
   Plan best;
   for (int id = 0; id < kNumKernels; ++id) {
     if (c->forced_kernel >= 0 && id != c->forced_kernel) continue;
@@ -319,6 +345,25 @@ Plan resolve(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bool h
       consider(c, id, epi, M, N, K, g, &best);
   }
   return best;
+}
+
+// The plan for a call: priced once per (M, N, K, epilogue, head64, conv)
+// and kept in the context, unless a kernel, grid or split is forced.  The
+// cache is cleared when it reaches kPlanCacheMax entries (ragged serving
+// sees many distinct M).
+constexpr size_t kPlanCacheMax = 1 << 14;
+
+Plan resolve(Context* c, int64_t M0, int64_t N, int64_t K, int epi, bool head64 = false, bool conv = false) {
+  if (c->forced_kernel >= 0 || c->forced_grid > 0 || c->forced_dp >= 0)
+    return price_plans(c, M0, N, K, epi, head64, conv);
+  const PlanKey key{M0, N, K, epi, head64, conv};
+  std::lock_guard<std::mutex> lock(c->plan_mu);
+  auto it = c->plans.find(key);
+  if (it != c->plans.end()) return it->second;
+  if (c->plans.size() >= kPlanCacheMax) c->plans.clear();
+  const Plan p = price_plans(c, M0, N, K, epi, head64, conv);
+  c->plans.emplace(key, p);
+  return p;
 }
 
 // Tile rows per raster group (tiles in flight together share x row panels
@@ -468,7 +513,7 @@ int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epi
   if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: null context");
   if (epi_id_from_flags(epilogue) < 0)
     return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: unsupported epilogue flags %d", epilogue);
-  const Context* c = static_cast<const Context*>(ctx);
+  Context* c = static_cast<Context*>(ctx);
   if (M <= 0 || N <= 0 || K <= 0)
     return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: bad shape");
   const Plan p = resolve(c, M, N, K, epi_id_from_flags(epilogue));
