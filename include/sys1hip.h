@@ -19,9 +19,11 @@
  *   - K, ldx and ldw must be multiples of 8 elements and x, w 16-byte
  *     aligned (128-bit loads).  y, residual and bias have no alignment rule
  *     beyond bf16's 2 bytes (aligned runs use 64-bit stores).  M may be 0.
- *   - The call allocates nothing and does not synchronise: work is enqueued on
- *     the context's stream (default: the context's own stream, or the one set
- *     by sys1hip_set_stream).
+ *   - The call allocates no device memory and does not synchronise: work is
+ *     enqueued on the context's stream (default: the context's own stream, or
+ *     the one set by sys1hip_set_stream).  The first call of a shape adds
+ *     its chosen kernel plan to the context's host-side plan cache (a small
+ *     heap allocation; calls of a known shape allocate nothing).
  *   - One context per stream.  Calls on one context must not overlap: the
  *     stream-K workspace and tile counters held by the context are shared
  *     by its calls.
