@@ -317,6 +317,8 @@ int64_t halo_rows(const KernelEntry& e, int64_t M, int halo) {
 
 // conv: only shapes with a conv epilogue (waves spanning every row), priced
 // on the rows their overlapping tile rows compute.
+constexpr int64_t kCachedWeightBytes = 32 << 20;
+
 Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bool head64, bool conv) {
   Plan best;
   for (int id = 0; id < kNumKernels; ++id) {
@@ -331,8 +333,13 @@ Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bo
       // the fabric), so stream-K is offered where M fits one tile row, or,
       // above 256 tokens, where the tiles cannot fill the CUs (few tiles,
       // deep K).  Up to 256 tokens the weight stream dominates, and a tile
-      // shorter than M would stream the weight once per tile row.
-      if (e.streamk && M > e.bm && (M <= 256 || cdiv(M, e.bm) * cdiv(N, e.bn) >= c->cus)) continue;
+      // shorter than M would stream the weight from HBM once per tile row;
+      // a weight of at most kCachedWeightBytes is re-read from L2 and MALL
+      // instead (measured: ModernBERT-large's mlp.Wo, 256x1024x2624, 17.8 us
+      // on 64-row stream tiles against 24.9 us on the best tile plan).
+      if (e.streamk && M > e.bm &&
+          ((M <= 256 && 2 * N * K > kCachedWeightBytes) || cdiv(M, e.bm) * cdiv(N, e.bn) >= c->cus))
+        continue;
       if (!e.streamk && M <= 128) continue;
     }
     const int64_t gmax = max_grid(c, id, epi, M, N, K);
