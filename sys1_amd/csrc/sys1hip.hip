@@ -244,7 +244,11 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
   // (A grid below one workgroup per CU leaves each workgroup's load latency
   // exposed: measured ~2200 cycles per k-tile for one 128x128 producer-wave
   // workgroup per CU streaming a cold weight.)
-  const double latency = e.pw && grid >= c->cus ? kProducerLatencyClk : kLatencyClk;
+  // A shape fitted for two workgroups per CU, alone on its CU (grid at most
+  // the CU count), is priced the same way: measured ~2160 cycles per k-tile
+  // for the 128x128 producer-wave shape on 256 tiles of 1024x2624.
+  const bool lone_pair = occupancy(c, id, epi) >= 2 && grid <= c->cus;
+  const double latency = e.pw && grid >= c->cus && !lone_pair ? kProducerLatencyClk : kLatencyClk;
   const double per_kt = std::max(share * std::max(mfma, load), latency / (e.stages - 1));
   const double store =
       e.streamk ? share * 2.0 * e.bm * e.bn / kStoreBytesPerClk
