@@ -351,7 +351,14 @@ Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bo
       consider(c, id, epi, M, N, K, std::min<int64_t>(c->forced_grid, gmax), &best);
       continue;
     }
-    const int64_t gmin = e.streamk && M <= e.bm ? std::max<int64_t>(1, gmax / 4) : gmax;
+    // A weight streamed from HBM (above kCachedWeightBytes) takes every CU:
+    // measured on the 27B projections at M = 128 and 256, the full stream-K
+    // grid was the fastest or within 3% of it, where the model's smaller
+    // grids (a quarter to a half of the CUs) ran up to 34% slower.  Small
+    // weights with short K keep the search (fewer owners per split tile).
+    const int64_t gmin = e.streamk && M <= e.bm && 2 * N * K <= kCachedWeightBytes
+                             ? std::max<int64_t>(1, gmax / 4)
+                             : gmax;
     for (int64_t g = gmax; g >= gmin; g -= std::max<int64_t>(1, gmax / 16))
       consider(c, id, epi, M, N, K, g, &best);
   }
