@@ -321,6 +321,41 @@ def test_residual_staged_in_lds_ragged_and_multi_tile(dev, orc, kname):
         dev.set_kernel(-1)
 
 
+def test_plan_cache_and_forcing(dev, orc):
+    """The chosen plan is cached per (M, N, K, epilogue).  A forced kernel or
+    grid bypasses the cache (the forced choice is reported and run), and
+    clearing the force returns the cached automatic choice.  Every call's
+    result matches the oracle, and repeated queries of several M return the
+    same choice as the first."""
+    from sys1_amd import kernel_names
+    from sys1_amd.linear import Linear
+    M, N, K = 300, 1024, 512
+    x, w = _inputs(orc, M, N, K, 91)
+    ref = orc.round_bf16(orc.linear_f64(orc.round_bf16(x), orc.round_bf16(w)).astype(np.float32))
+    lin = Linear(to_gpu_bf16(w, torch), device=dev)
+    xg = to_gpu_bf16(x, torch)
+    auto = dev.query_kernel(M, N, K)
+    assert_parity(to_np(lin(xg)), ref, "auto")
+    assert dev.query_kernel(M, N, K) == auto
+    other = next(i for i, n in enumerate(kernel_names()) if i != auto[0] and n.startswith("tile_"))
+    try:
+        dev.set_kernel(other)
+        assert dev.query_kernel(M, N, K)[0] == other
+        assert_parity(to_np(lin(xg)), ref, f"forced {kernel_names()[other]}")
+        dev.set_kernel(-1)
+        dev.set_grid(3)
+        assert "_g3" in dev.query_kernel(M, N, K)[1]
+        assert_parity(to_np(lin(xg)), ref, "forced grid 3")
+    finally:
+        dev.set_kernel(-1)
+        dev.set_grid(0)
+    assert dev.query_kernel(M, N, K) == auto
+    assert_parity(to_np(lin(xg)), ref, "auto again")
+    picks = {m: dev.query_kernel(m, N, K) for m in (1, 64, 128, 256, 1024, 8192)}
+    for m, p in picks.items():
+        assert dev.query_kernel(m, N, K) == p
+
+
 def test_gelu_every_bf16_input(dev, orc):
     """The GeGLU epilogue's GELU over every finite bf16 gate value (the gate is
     the bf16-rounded projection, so these are all the inputs it can see),
