@@ -322,6 +322,7 @@ int64_t halo_rows(const KernelEntry& e, int64_t M, int halo) {
 // conv: only shapes with a conv epilogue (waves spanning every row), priced
 // on the rows their overlapping tile rows compute.
 constexpr int64_t kCachedWeightBytes = 32 << 20;
+constexpr int64_t kRereadWeightBytes = 128 << 20;  // half the 256 MB MALL
 
 Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bool head64, bool conv) {
   Plan best;
@@ -341,8 +342,12 @@ Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bo
       // a weight of at most kCachedWeightBytes is re-read from L2 and MALL
       // instead (measured: ModernBERT-large's mlp.Wo, 256x1024x2624, 17.8 us
       // on 64-row stream tiles against 24.9 us on the best tile plan).
-      if (e.streamk && M > e.bm &&
-          ((M <= 256 && 2 * N * K > kCachedWeightBytes) || cdiv(M, e.bm) * cdiv(N, e.bn) >= c->cus))
+      // Up to kRereadWeightBytes, two tile rows (one re-read, from MALL)
+      // still pay: the 27B out_proj at M = 256 (63 MB) ran 41.8 us on
+      // 128-row stream tiles against 77 us on the best tile plan.
+      const bool reread_ok = 2 * N * K <= kCachedWeightBytes ||
+                             (2 * N * K <= kRereadWeightBytes && cdiv(M, e.bm) <= 2);
+      if (e.streamk && M > e.bm && ((M <= 256 && !reread_ok) || cdiv(M, e.bm) * cdiv(N, e.bn) >= c->cus))
         continue;
       if (!e.streamk && M <= 128) continue;
     }
