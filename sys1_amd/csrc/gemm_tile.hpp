@@ -46,6 +46,7 @@
 //          deterministic whatever the arrival order -- applies the epilogue
 //          to it and re-arms the counter.
 #pragma once
+#define SYS1_GEMM_TILE_HPP
 
 #include <type_traits>
 

@@ -14,7 +14,7 @@
 #include <vector>
 
 #include "common.hpp"
-#include "gemm_tile.hpp"
+#include "kernel_fns.hpp"
 #include "norm.hpp"
 #include "conv.hpp"
 
@@ -93,8 +93,6 @@ struct Context {
   std::unordered_map<PlanKey, Plan, PlanKeyHash> plans;
 };
 
-using KernelFn = void (*)(GemmArgs);
-
 struct KernelEntry {
   const char* name;
   int bm, bn, threads;
@@ -109,66 +107,24 @@ struct KernelEntry {
   int pw;               // producer waves (0: the compute waves issue the refills)
   float swiglu_efficiency;  // efficiency with a SwiGLU epilogue, when it differs (0: the same)
   float long_k_efficiency;  // efficiency for K > kLongK, when it differs (0: the same)
-  KernelFn fn[kEpiCount];
+  const KernelFn* fn;   // [kEpiCount]: the shape's kernel per epilogue (null: not built)
 };
 
-// The conv epilogues exist for shapes whose waves hold every row of a tile.
-template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK, int EPI, int PW>
-constexpr KernelFn conv_fn() {
-  if constexpr (WM == 1 && PW == 0) return gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, EPI, PW>;
-  else return nullptr;
-}
+}  // namespace
 
-// PW: producer waves (see gemm_tile_kernel).
-template <int BM, int BN, int WM, int WN, int ST, int BK, int OCC, bool SK, int PW = 0>
-constexpr KernelEntry tile_entry(const char* name, float eff, float swiglu_eff = 0.0f, float long_k_eff = 0.0f) {
-  return KernelEntry{name, BM, BN, (WM * WN + PW) * 64, OCC, SK, eff, BK, ST, BN / WN, WM, PW, swiglu_eff, long_k_eff,
-                     {gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 0, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 1, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 2, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 3, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 4, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 5, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 6, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 7, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 8, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 9, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 10, PW>,
-                      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 11, PW>,
-                      conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 12, PW>(),
-                      conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 13, PW>()}};
-}
+// Each shape's kernels are compiled in a translation unit of their own.
+#define SYS1_SHAPE(name, BM, BN, WM, WN, ST, BK, OCC, SK, PW, EFF, SWEFF, LKEFF) SYS1_DECLARE_SHAPE(name)
+#include "shapes.def"
+#undef SYS1_SHAPE
 
-// Output-tile shapes.  The first group serves large M (MFMA-bound); the
-// "stream" group serves small M (weight-streaming: BM = padded token count,
-// BN = 256, deep stages, K split over workgroups).
+namespace {
+
+// Output-tile shapes, in the order of shapes.def (the kernel ids).
 const KernelEntry kKernels[] = {
-    // Large M.  _p4: four producer waves issue the refills (see gemm_tile_kernel).
-    tile_entry<256, 256, 2, 4, 2, 64, 1, false>("tile_256x256_s2_w2x4", 0.80f),
-    // (one fragment set: measured ~10% slower than the plain 256x256 except
-    // with the SwiGLU epilogues, where it is ~10% faster; with GeGLU's erf it
-    // spills and runs at half speed)
-    tile_entry<256, 256, 2, 4, 2, 64, 1, false, 4>("tile_256x256_s2_w2x4_p4", 0.70f, 0.88f),
-    tile_entry<128, 256, 2, 4, 3, 64, 1, false, 4>("tile_128x256_s3_w2x4_p4", 0.50f),
-    tile_entry<256, 128, 2, 2, 3, 64, 1, false, 4>("tile_256x128_s3_w2x2_p4", 0.74f),
-    tile_entry<128, 128, 2, 2, 2, 64, 2, false, 4>("tile_128x128_s2_w2x2_p4", 0.70f),
-    tile_entry<128, 128, 2, 2, 2, 64, 2, false>("tile_128x128_s2_w2x2", 0.60f),
-    tile_entry<128, 96, 4, 1, 2, 64, 2, false, 4>("tile_128x96_s2_w4x1_p4", 0.53f),
-    tile_entry<128, 192, 4, 2, 3, 64, 1, false, 4>("tile_128x192_s3_w4x2_p4", 0.60f),
-    // (two stages only: with K beyond a few thousand its panels stream from
-    // beyond the L2 and the one k-tile in flight exposes the latency)
-    tile_entry<256, 192, 4, 2, 2, 64, 1, false, 4>("tile_256x192_s2_w4x2_p4", 0.80f, 0.0f, 0.60f),
-    tile_entry<256, 160, 8, 1, 3, 64, 1, false, 4>("tile_256x160_s3_w8x1_p4", 0.80f),
-    tile_entry<32, 256, 1, 4, 4, 64, 1, true>("stream_32x256_s4_w1x4", 0.50f),
-    tile_entry<64, 256, 2, 4, 3, 64, 1, true>("stream_64x256_s3_w2x4", 0.60f),
-    tile_entry<64, 256, 2, 4, 4, 64, 1, true>("stream_64x256_s4_w2x4", 0.60f),
-    tile_entry<128, 128, 2, 2, 4, 64, 1, true>("stream_128x128_s4_w2x2", 0.80f),
-    tile_entry<128, 256, 2, 4, 3, 64, 1, true>("stream_128x256_s3_w2x4", 0.80f),
-    tile_entry<256, 128, 4, 2, 3, 64, 1, true>("stream_256x128_s3_w4x2", 0.80f),
-    // Waves span every row of the tile (WM = 1): the shapes of the DeltaNet
-    // in_proj with its causal conv fused (the conv reads earlier rows).
-    tile_entry<128, 256, 1, 4, 2, 64, 1, false>("tile_128x256_s2_w1x4", 0.30f),
-    tile_entry<128, 256, 1, 4, 3, 64, 1, true>("stream_128x256_s3_w1x4", 0.30f),
+#define SYS1_SHAPE(name, BM, BN, WM, WN, ST, BK, OCC, SK, PW, EFF, SWEFF, LKEFF) \
+  KernelEntry{#name, BM, BN, (WM * WN + PW) * 64, OCC, SK, EFF, BK, ST, BN / WN, WM, PW, SWEFF, LKEFF, sys1::name##_fns},
+#include "shapes.def"
+#undef SYS1_SHAPE
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
