@@ -156,6 +156,41 @@ __host__ __device__ constexpr bool epi_has_resid() {
   return EPI == kEpiResidual || EPI == kEpiBiasResidual;
 }
 
+// ---- buffer and LDS-DMA helpers shared by the GEMM kernels.
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Raw buffer descriptor over [base, base + 2 GiB): offsets at or past
+// kOutOfRange fall outside it and read as zeros.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr unsigned kOutOfRange = 0x80000000u;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes = 0x7ffffff0) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+// The same from values the caller knows to be wave-uniform, moved to SGPRs
+// explicitly: a descriptor the compiler cannot prove uniform is otherwise
+// consumed through a readfirstlane loop around every load.
+__device__ __forceinline__ rsrc_t make_rsrc_uniform(const void* base, int bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  return make_rsrc(reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo),
+                   __builtin_amdgcn_readfirstlane(bytes));
+}
+
+// Asynchronous 16-byte-per-lane copy global -> LDS: lane i's 16 bytes (from
+// byte offset `off` of the buffer) land at lds_base + 16 * i; lds_base is
+// wave-uniform.
+__device__ __forceinline__ void dma16(rsrc_t r, unsigned off, lds_void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_base, 16, (int)off, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) with the LDS and export counters left unconstrained.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
 // Arguments shared by every GEMM kernel.
 struct GemmArgs {
   const __bf16* x;      // [M, K], ld ldx

@@ -48,3 +48,29 @@ constexpr KernelFn conv_fn() {
       conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 13, PW>()};                                        \
   }
 #endif
+
+#ifdef SYS1_SKINNY_HPP
+namespace sys1 {
+// A skinny-M kernel per epilogue; null where the epilogue does not apply
+// (gated epilogues need two 16-row blocks; RoPE and conv run on the tile
+// kernels).
+template <int FM, int FN, int NW, int U, int EPI>
+constexpr KernelFn skinny_fn() {
+  if constexpr ((epi_gated(EPI) && FN != 2) || epi_base(EPI) == kEpiRopeQkv || epi_base(EPI) == kEpiConvSilu)
+    return nullptr;
+  else
+    return skinny_kernel<FM, FN, NW, U, EPI>;
+}
+}  // namespace sys1
+
+#define SYS1_DEFINE_SKINNY(name, FM, FN, NW, U)                                                              \
+  namespace sys1 {                                                                                          \
+  extern const KernelFn name##_fns[kEpiCount];                                                              \
+  const KernelFn name##_fns[kEpiCount] = {                                                                  \
+      skinny_fn<FM, FN, NW, U, 0>(),  skinny_fn<FM, FN, NW, U, 1>(),  skinny_fn<FM, FN, NW, U, 2>(),        \
+      skinny_fn<FM, FN, NW, U, 3>(),  skinny_fn<FM, FN, NW, U, 4>(),  skinny_fn<FM, FN, NW, U, 5>(),        \
+      skinny_fn<FM, FN, NW, U, 6>(),  skinny_fn<FM, FN, NW, U, 7>(),  skinny_fn<FM, FN, NW, U, 8>(),        \
+      skinny_fn<FM, FN, NW, U, 9>(),  skinny_fn<FM, FN, NW, U, 10>(), skinny_fn<FM, FN, NW, U, 11>(),       \
+      skinny_fn<FM, FN, NW, U, 12>(), skinny_fn<FM, FN, NW, U, 13>()};                                      \
+  }
+#endif

@@ -57,8 +57,10 @@ struct PlanKey {
   int64_t M, N, K;
   int epi;
   bool head64, conv;
+  bool wide_w;  // weight rows span 2 GiB or more (the skinny kernels' offsets would not reach)
   bool operator==(const PlanKey& o) const {
-    return M == o.M && N == o.N && K == o.K && epi == o.epi && head64 == o.head64 && conv == o.conv;
+    return M == o.M && N == o.N && K == o.K && epi == o.epi && head64 == o.head64 && conv == o.conv &&
+           wide_w == o.wide_w;
   }
 };
 
@@ -67,7 +69,7 @@ struct PlanKeyHash {
     uint64_t h = (uint64_t)k.M * 0x9E3779B97F4A7C15ull;
     h ^= ((uint64_t)k.N * 0xC2B2AE3D27D4EB4Full) + (h << 6) + (h >> 2);
     h ^= ((uint64_t)k.K * 0x165667B19E3779F9ull) + (h << 6) + (h >> 2);
-    h ^= (uint64_t)(k.epi * 4 + k.head64 * 2 + k.conv) + (h << 6) + (h >> 2);
+    h ^= (uint64_t)(k.epi * 8 + k.wide_w * 4 + k.head64 * 2 + k.conv) + (h << 6) + (h >> 2);
     return (size_t)h;
   }
 };
@@ -108,23 +110,30 @@ struct KernelEntry {
   float swiglu_efficiency;  // efficiency with a SwiGLU epilogue, when it differs (0: the same)
   float long_k_efficiency;  // efficiency for K > kLongK, when it differs (0: the same)
   const KernelFn* fn;   // [kEpiCount]: the shape's kernel per epilogue (null: not built)
+  bool skinny;          // skinny-M kernel (skinny.hpp): one workgroup per bn columns, all rows
 };
 
 }  // namespace
 
 // Each shape's kernels are compiled in a translation unit of their own.
 #define SYS1_SHAPE(name, BM, BN, WM, WN, ST, BK, OCC, SK, PW, EFF, SWEFF, LKEFF) SYS1_DECLARE_SHAPE(name)
+#define SYS1_SKINNY(name, FM, FN, NW, U) SYS1_DECLARE_SHAPE(name)
 #include "shapes.def"
 #undef SYS1_SHAPE
+#undef SYS1_SKINNY
 
 namespace {
 
 // Output-tile shapes, in the order of shapes.def (the kernel ids).
 const KernelEntry kKernels[] = {
 #define SYS1_SHAPE(name, BM, BN, WM, WN, ST, BK, OCC, SK, PW, EFF, SWEFF, LKEFF) \
-  KernelEntry{#name, BM, BN, (WM * WN + PW) * 64, OCC, SK, EFF, BK, ST, BN / WN, WM, PW, SWEFF, LKEFF, sys1::name##_fns},
+  KernelEntry{#name, BM, BN, (WM * WN + PW) * 64, OCC, SK, EFF, BK, ST, BN / WN, WM, PW, SWEFF, LKEFF, sys1::name##_fns, false},
+// (skinny entries: tn 16 and wm 0 keep the RoPE and fused-conv calls off them)
+#define SYS1_SKINNY(name, FM, FN, NW, U) \
+  KernelEntry{#name, 16 * FM, 16 * FN, NW * 64, 1, false, 1.0f, 32, 0, 16, 0, 0, 0.0f, 0.0f, sys1::name##_fns, true},
 #include "shapes.def"
 #undef SYS1_SHAPE
+#undef SYS1_SKINNY
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
@@ -228,6 +237,7 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
 
 int64_t max_grid(const Context* c, int id, int epi, int64_t M, int64_t N, int64_t K) {
   const KernelEntry& e = kKernels[id];
+  if (e.skinny) return cdiv(N, e.bn);  // one workgroup per bn columns
   const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
   int64_t g = (int64_t)c->cus * occupancy(c, id, epi);
   if (!e.streamk) return std::min(g, tiles);
@@ -280,11 +290,56 @@ int64_t halo_rows(const KernelEntry& e, int64_t M, int halo) {
 constexpr int64_t kCachedWeightBytes = 32 << 20;
 constexpr int64_t kRereadWeightBytes = 128 << 20;  // half the 256 MB MALL
 
-Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bool head64, bool conv) {
+// The skinny-M kernel for a call, or -1.  Each skinny workgroup reads its
+// bn weight rows and all of x over the whole K, so a CU moves
+//   ceil(workgroups / CUs) * (rows + bn) * K * 2 bytes
+// through its load path; the kernel wins while that stays within
+// kSkinnyCuBytes (measured over the ModernBERT-base/large and Qwen3.5-small
+// projections at M = 16..128: 295-420 KB per CU ran 1.1-1.7x faster than
+// the stream-K kernels, 590-655 KB tied, 756 KB and above lost).  Above
+// kSkinnyWeightBytes the weight is streamed from HBM and needs the
+// stream-K schedule's spread of K over every CU.  The rows are the smallest
+// 16 FM >= M; non-gated calls take the 16- or 32-column shape that moves
+// fewer bytes per CU (16 on a tie: more workgroups in flight), gated calls
+// the 32-column one (one gate/up row group per workgroup).
+constexpr int64_t kSkinnyMaxM = 128;
+constexpr int64_t kSkinnyWeightBytes = 32 << 20;
+constexpr int64_t kSkinnyCuBytes = 512 << 10;
+
+int skinny_pick(const Context* c, int64_t M, int64_t N, int64_t K, int64_t ldw, int epi) {
+  if (M > kSkinnyMaxM || 2 * N * K > kSkinnyWeightBytes || 2 * N * ldw >= 0x7ffffff0ll) return -1;
+  const int64_t bm = M <= 16 ? 16 : M <= 32 ? 32 : M <= 64 ? 64 : 128;
+  auto cu_bytes = [&](int64_t bn) { return cdiv(cdiv(N, bn), c->cus) * (bm + bn) * K * 2; };
+  int64_t bn = 32;
+  if (!epi_gated(epi) && cu_bytes(16) <= cu_bytes(32)) bn = 16;
+  if (cu_bytes(bn) > kSkinnyCuBytes) return -1;
+  for (int id = 0; id < kNumKernels; ++id) {
+    const KernelEntry& e = kKernels[id];
+    if (e.skinny && e.bm == bm && e.bn == bn && e.fn[epi]) return id;
+  }
+  return -1;
+}
+
+Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int64_t ldw, int epi, bool head64,
+                 bool conv) {
   Plan best;
+  if (c->forced_kernel < 0 && !head64 && !conv) {
+    const int id = skinny_pick(c, M0, N, K, ldw, epi);
+    if (id >= 0) {
+      best.kernel = id, best.grid = cdiv(N, kKernels[id].bn), best.dp = 0, best.cost = 0.0;
+      return best;
+    }
+  }
   for (int id = 0; id < kNumKernels; ++id) {
     if (c->forced_kernel >= 0 && id != c->forced_kernel) continue;
     const KernelEntry& e = kKernels[id];
+    if (!e.fn[epi]) continue;
+    if (e.skinny) {
+      // (only when forced: the automatic choice is skinny_pick's)
+      if (c->forced_kernel != id || M0 > e.bm || head64 || conv || 2 * N * ldw >= 0x7ffffff0ll) continue;
+      best.kernel = id, best.grid = cdiv(N, e.bn), best.dp = 0, best.cost = 0.0;
+      continue;
+    }
     if (head64 && e.tn != 64) continue;
     if (conv && e.wm != 1) continue;
     const int64_t M = conv ? halo_rows(e, M0, kConvHalo) : M0;
@@ -323,6 +378,7 @@ Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bo
     for (int64_t g = gmax; g >= gmin; g -= std::max<int64_t>(1, gmax / 16))
       consider(c, id, epi, M, N, K, g, &best);
   }
+  if (best.cost == 1e300) best.kernel = -1;  // (a forced kernel that cannot run the call)
   return best;
 }
 
@@ -332,15 +388,16 @@ Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int epi, bo
 // sees many distinct M).
 constexpr size_t kPlanCacheMax = 1 << 14;
 
-Plan resolve(Context* c, int64_t M0, int64_t N, int64_t K, int epi, bool head64 = false, bool conv = false) {
+Plan resolve(Context* c, int64_t M0, int64_t N, int64_t K, int64_t ldw, int epi, bool head64 = false,
+             bool conv = false) {
   if (c->forced_kernel >= 0 || c->forced_grid > 0 || c->forced_dp >= 0)
-    return price_plans(c, M0, N, K, epi, head64, conv);
-  const PlanKey key{M0, N, K, epi, head64, conv};
+    return price_plans(c, M0, N, K, ldw, epi, head64, conv);
+  const PlanKey key{M0, N, K, epi, head64, conv, 2 * N * ldw >= 0x7ffffff0ll};
   std::lock_guard<std::mutex> lock(c->plan_mu);
   auto it = c->plans.find(key);
   if (it != c->plans.end()) return it->second;
   if (c->plans.size() >= kPlanCacheMax) c->plans.clear();
-  const Plan p = price_plans(c, M0, N, K, epi, head64, conv);
+  const Plan p = price_plans(c, M0, N, K, ldw, epi, head64, conv);
   c->plans.emplace(key, p);
   return p;
 }
@@ -495,8 +552,9 @@ int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epi
   Context* c = static_cast<Context*>(ctx);
   if (M <= 0 || N <= 0 || K <= 0)
     return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: bad shape");
-  const Plan p = resolve(c, M, N, K, epi_id_from_flags(epilogue));
+  const Plan p = resolve(c, M, N, K, K, epi_id_from_flags(epilogue));
   const int id = p.kernel;
+  if (id < 0) return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: the forced kernel does not fit this call");
   if (name && cap > 0) {
     std::string s = kKernels[id].name;
     s += "_g" + std::to_string(p.grid);
@@ -545,7 +603,8 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
 
   int rc = use_device(c);
   if (rc) return rc;
-  const Plan p = resolve(c, M, N, K, epi);
+  const Plan p = resolve(c, M, N, K, ldw, epi);
+  if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: the forced kernel does not fit this call");
   const KernelEntry& e = kKernels[p.kernel];
   const int64_t grid = p.grid;
   if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
@@ -601,7 +660,8 @@ int sys1hip_linear_rope_qkv_bf16(void* ctx, const uint16_t* x, int64_t ldx, cons
   if (c->forced_kernel >= 0 && kKernels[c->forced_kernel].tn != 64)
     return fail(SYS1HIP_EINVAL, "sys1hip_linear_rope_qkv_bf16: forced kernel %s is not head-aligned",
                 kKernels[c->forced_kernel].name);
-  const Plan p = resolve(c, M, N, K, kEpiRopeQkv, true);
+  const Plan p = resolve(c, M, N, K, ldw, kEpiRopeQkv, true);
+  if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_linear_rope_qkv_bf16: the forced kernel does not fit this call");
   const KernelEntry& e = kKernels[p.kernel];
   if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
     return fail(SYS1HIP_ERANGE, "sys1hip_linear_rope_qkv_bf16: more split tiles than stream-K counters");
@@ -715,7 +775,8 @@ int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const ui
     return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: dimension above 2^30");
   int rc = use_device(c);
   if (rc) return rc;
-  const Plan p = resolve(c, M, N, K, epi);
+  const Plan p = resolve(c, M, N, K, ldw, epi);
+  if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: the forced kernel does not fit this call");
   const KernelEntry& e = kKernels[p.kernel];
   if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
     return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: more split tiles than stream-K counters");
@@ -791,7 +852,8 @@ int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx, con
   // shapes lose more in the GEMM than the fused form saves in traffic.
   const bool fused = c->forced_kernel >= 0 && kKernels[c->forced_kernel].wm == 1;
   const int epi = fused ? (norm ? kEpiNormRmsConvSilu : kEpiConvSilu) : (norm ? kEpiNormRms : kEpiNone);
-  const Plan p = resolve(c, M, N, K, epi, false, fused);
+  const Plan p = resolve(c, M, N, K, ldw, epi, false, fused);
+  if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: the forced kernel does not fit this call");
   const KernelEntry& e = kKernels[p.kernel];
   if (!e.fn[epi])
     return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: kernel %s has no conv epilogue", e.name);

@@ -73,11 +73,17 @@ def test_every_kernel_every_epilogue(dev, orc, kid, name):
     """Force each kernel id and check every epilogue on ragged shapes."""
     from sys1_amd import _lib
     from sys1_amd.linear import GatedLinear, Linear
+    skinny = name.startswith("skinny_")
     if name.startswith("stream_"):
         cap = int(name.split("_")[1].split("x")[0])
         Ms = sorted({max(1, cap // 2 + 3), cap, 300})
+    elif skinny:  # M up to the kernel's rows (a forced skinny kernel refuses more)
+        cap = int(name.split("_")[1].split("x")[0])
+        Ms = sorted({1, max(1, cap // 2 + 3), cap})
     else:
         Ms = [300, 513]
+    # (a two-block skinny kernel is the one that runs the gated epilogues)
+    gated_ok = not skinny or name.split("_")[1].endswith("x32")
     dev.set_kernel(kid)
     try:
         for M in Ms:
@@ -110,6 +116,8 @@ def test_every_kernel_every_epilogue(dev, orc, kid, name):
             # bias + gelu (Laya scorer_in)
             y = to_np(Linear(wg, to_gpu_bf16(bias, torch), device=dev)(xg, gelu=True))
             assert_parity(y, orc.round_bf16(orc.gelu_erf(orc.round_bf16(p16 + bb))), f"{name} bias+gelu")
+            if not gated_ok:
+                continue
             # gated: GeGLU and SwiGLU over [2I, K] = [gate; up], I = N/2
             I = N // 2
             g16, u16 = p16[:, :I], p16[:, I:]
@@ -269,7 +277,7 @@ def test_tile_kernel_small_forced_grid(dev, orc):
 
 
 @pytest.mark.parametrize("kname", [n for n in __import__("sys1_amd").kernel_names()
-                                   if not n.startswith("stream_")])
+                                   if n.startswith("tile_")])
 def test_tile_kernels_short_k_and_small_grids(dev, orc, kname):
     """Streams of 1..6 k-tiles per tile and 1..n tiles per workgroup: the
     pipeline prologue and refill cursors at every stream length."""
@@ -439,3 +447,42 @@ def test_python_errors(dev, orc):
     assert e.value.code == -14
     with pytest.raises(ValueError):
         GatedLinear(torch.zeros(80, 64, dtype=torch.bfloat16, device="cuda:0"), device=dev)
+
+
+@pytest.mark.parametrize("kname", [n for n in __import__("sys1_amd").kernel_names()
+                                   if n.startswith("skinny_")])
+def test_skinny_kernels_ragged_shapes(dev, orc, kname):
+    """The skinny-M kernels: K split over the waves with empty, one-step and
+    tail (K % 32 != 0) ranges, N not a multiple of the 16-column block (the
+    last workgroup's rows clamped, its columns stored element by element),
+    every M up to the kernel's rows, and repeated calls bit-identical (the
+    waves' partials are summed in a fixed order)."""
+    from sys1_amd import kernel_names
+    from sys1_amd.linear import GatedLinear, Linear
+    cap = int(kname.split("_")[1].split("x")[0])
+    two_block = kname.split("_")[1].endswith("x32")
+    dev.set_kernel(kernel_names().index(kname))
+    try:
+        for (M, N, K) in [(1, 1, 40), (cap, 17, 72), (max(1, cap - 5), 520, 136), (cap, 1000, 1000),
+                          (min(cap, 7), 48, 4104), (cap, 64, 8)]:
+            print(f"[gpu] {kname} M={M} N={N} K={K}", flush=True)
+            x, w = _inputs(orc, M, N, K, 91 + M + K)
+            proj = orc.linear_f64(orc.round_bf16(x), orc.round_bf16(w)).astype(np.float32)
+            lin = Linear(to_gpu_bf16(w, torch), device=dev)
+            xg = to_gpu_bf16(x, torch)
+            y = to_np(lin(xg))
+            _check_close_to_rounded(orc, y, proj, f"{kname} M={M} N={N} K={K}")
+            np.testing.assert_array_equal(y, to_np(lin(xg)))
+            if two_block and N % 32 == 0:
+                p16 = orc.round_bf16(proj)
+                I = N // 2
+                ref = orc.round_bf16(orc.round_bf16(orc.silu(p16[:, :I])) * p16[:, I:])
+                assert_parity(to_np(GatedLinear(to_gpu_bf16(w, torch), "silu", device=dev)(xg)), ref,
+                              f"{kname} swiglu M={M} N={N} K={K}")
+        # more rows than the kernel holds: the forced call is refused, not run
+        from sys1_amd import _lib
+        x, w = _inputs(orc, cap + 1, 64, 64, 5)
+        with pytest.raises(_lib.Sys1HipError):
+            Linear(to_gpu_bf16(w, torch), device=dev)(to_gpu_bf16(x, torch))
+    finally:
+        dev.set_kernel(-1)
