@@ -77,7 +77,12 @@ SYS1HIP_API int sys1hip_destroy(void* ctx);
 
 /* Enqueue subsequent work on `stream` (a hipStream_t; NULL is HIP's null
  * stream).  Lets a caller share the stream of the framework that owns the
- * buffers (e.g. torch's current stream). */
+ * buffers (e.g. torch's current stream).  When the stream changes, the new
+ * stream is made to wait for the work already enqueued on the old one (an
+ * event recorded there), so calls before and after the switch never overlap
+ * on the context's shared workspace.  While either stream is being captured
+ * into a HIP graph no wait is inserted: ordering a captured graph's replays
+ * against eager work on another stream is then the caller's. */
 SYS1HIP_API int sys1hip_set_stream(void* ctx, void* stream);
 
 /* Block until the context's stream is idle. */

@@ -78,6 +78,7 @@ struct Context {
   int device = 0;
   hipStream_t own = nullptr;
   hipStream_t stream = nullptr;
+  hipEvent_t order = nullptr;  // orders a new stream after the old one (sys1hip_set_stream)
   float* ws = nullptr;
   unsigned* counters = nullptr;
   float* stats = nullptr;  // pre-norm row statistics, kNormRows x (mean, 1/std)
@@ -464,6 +465,7 @@ int sys1hip_init(int device, void** out) {
   if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
     c->cus = prop.multiProcessorCount;
   if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&c->order, hipEventDisableTiming) != hipSuccess ||
       hipMalloc(&c->ws, kWorkspaceBytes) != hipSuccess ||
       hipMalloc(&c->counters, kCounterSlots * sizeof(unsigned)) != hipSuccess ||
       hipMalloc(&c->stats, kNormRows * 2 * sizeof(float)) != hipSuccess ||
@@ -473,6 +475,7 @@ int sys1hip_init(int device, void** out) {
     if (c->stats) (void)hipFree(c->stats);
     if (c->counters) (void)hipFree(c->counters);
     if (c->ws) (void)hipFree(c->ws);
+    if (c->order) (void)hipEventDestroy(c->order);
     if (c->own) (void)hipStreamDestroy(c->own);
     delete c;
     return fail(SYS1HIP_EDEVICE, "sys1hip_init: device set-up failed (%s)", msg);
@@ -501,6 +504,7 @@ int sys1hip_destroy(void* ctx) {
   (void)hipFree(c->stats);
   (void)hipFree(c->counters);
   (void)hipFree(c->ws);
+  (void)hipEventDestroy(c->order);
   (void)hipStreamDestroy(c->own);
   delete c;
   return SYS1HIP_OK;
@@ -509,7 +513,22 @@ int sys1hip_destroy(void* ctx) {
 int sys1hip_set_stream(void* ctx, void* stream) {
   if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_set_stream: null context");
   Context* c = static_cast<Context*>(ctx);
-  c->stream = static_cast<hipStream_t>(stream);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (s == c->stream) return SYS1HIP_OK;
+  int rc = use_device(c);
+  if (rc) return rc;
+  // The context's workspace, counters and row statistics are shared by all
+  // its calls: work enqueued after the switch waits for work enqueued
+  // before it.  (Not while a graph is being captured on either stream: a
+  // wait on an event from outside the capture is not capturable.)
+  hipStreamCaptureStatus old_st = hipStreamCaptureStatusNone, new_st = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(c->stream, &old_st));
+  HIP_TRY(hipStreamIsCapturing(s, &new_st));
+  if (old_st == hipStreamCaptureStatusNone && new_st == hipStreamCaptureStatusNone) {
+    HIP_TRY(hipEventRecord(c->order, c->stream));
+    HIP_TRY(hipStreamWaitEvent(s, c->order, 0));
+  }
+  c->stream = s;
   return SYS1HIP_OK;
 }
 

@@ -486,3 +486,34 @@ def test_skinny_kernels_ragged_shapes(dev, orc, kname):
             Linear(to_gpu_bf16(w, torch), device=dev)(to_gpu_bf16(x, torch))
     finally:
         dev.set_kernel(-1)
+
+
+def test_stream_switch_waits_for_the_old_stream(dev, orc):
+    """sys1hip_set_stream (via HipDevice.follow_torch_stream) makes the new
+    stream wait for the work queued on the old one: the context's workspace
+    and counters are shared by all its calls.  A long spin queued on stream
+    A holds back work queued on stream B after the switch."""
+    from sys1_amd.linear import Linear
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    x, w = _inputs(orc, 64, 256, 256, 3)
+    lin = Linear(to_gpu_bf16(w, torch), device=dev)
+    xg = to_gpu_bf16(x, torch)
+    torch.cuda.synchronize()
+    try:
+        with torch.cuda.stream(a):
+            dev.follow_torch_stream()
+            torch.cuda._sleep(200_000_000)  # ~0.1 s of spinning on A
+            ya = lin(xg)
+        with torch.cuda.stream(b):
+            dev.follow_torch_stream()  # the switch: B waits for A's queue
+            yb = lin(xg)
+            done = torch.cuda.Event()
+            done.record(b)
+        print(f"[gpu] stream switch: B done before A's spin ended: {done.query()}", flush=True)
+        assert not done.query(), "work on the new stream ran before the old stream's queue"
+        torch.cuda.synchronize()
+        assert done.query()
+        assert torch.equal(ya, yb)
+    finally:
+        torch.cuda.synchronize()
+        dev.follow_torch_stream()
