@@ -221,6 +221,31 @@ SYS1HIP_API int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int6
  * 0 is pure stream-K; the tile count is the plain tile schedule. */
 SYS1HIP_API int sys1hip_set_dp_tiles(void* ctx, int32_t tiles);
 
+/* sys1hip_linear_bf16 without a context, allocating nothing.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, checks, arithmetic and
+ * kernel choice as sys1hip_linear_bf16, on the current HIP device, enqueued
+ * on `stream` (a hipStream_t, NULL = the null stream).  Its stream-K
+ * workspace is a static device array of 64 MB of partials plus 65536
+ * arrival counters (64.25 MB in all), one per GPU, held from the first call
+ * on that GPU until the process ends; the kernel plan is limited to that
+ * workspace, and a call that would need more split tiles than there are
+ * counters is refused (SYS1HIP_ERANGE).  The first call on a device looks
+ * up the array's address and the kernels' occupancy (and clears the
+ * counters when not under capture); it allocates nothing either.  Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (on
+ * different streams, or from several threads) race on it and must not.
+ * Errors: as sys1hip_linear_bf16, message from sys1hip_last_error(NULL). */
+SYS1HIP_API int sys1hip_linear_bf16_noalloc(void* stream,
+                        const uint16_t* x, int64_t ldx,
+                        const uint16_t* w, int64_t ldw,
+                        const uint16_t* bias,
+                        const uint16_t* residual, int64_t ldr,
+                        uint16_t* y, int64_t ldy,
+                        int64_t M, int64_t N, int64_t K,
+                        int32_t epilogue);
+
 /* Number of kernel ids and the name of one id (for sweeps). */
 SYS1HIP_API int sys1hip_kernel_count(void);
 SYS1HIP_API const char* sys1hip_kernel_name(int32_t kernel_id);

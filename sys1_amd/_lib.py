@@ -37,7 +37,7 @@ EXPORTS = (
     "sys1hip_pack_gated_weight", "sys1hip_query_kernel", "sys1hip_set_kernel",
     "sys1hip_kernel_count", "sys1hip_kernel_name", "sys1hip_set_grid",
     "sys1hip_set_dp_tiles", "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
-    "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16",
+    "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_linear_bf16_noalloc",
 )
 
 
@@ -71,6 +71,8 @@ def load() -> ctypes.CDLL:
     L.sys1hip_last_error.argtypes = [vp]
     L.sys1hip_last_error.restype = ctypes.c_char_p
     L.sys1hip_linear_bf16.argtypes = [vp, vp, i64, vp, i64, vp, vp, i64, vp, i64, i64, i64, i64, i32]
+    L.sys1hip_linear_bf16_noalloc.argtypes = [vp, vp, i64, vp, i64, vp, vp, i64, vp, i64, i64, i64, i64,
+                                              i32]
     L.sys1hip_pack_gated_weight.argtypes = [vp, vp, vp, i64, i64]
     L.sys1hip_query_kernel.argtypes = [vp, i64, i64, i64, i32, ctypes.c_char_p, i64]
     L.sys1hip_set_kernel.argtypes = [vp, i32]
@@ -89,7 +91,8 @@ def load() -> ctypes.CDLL:
                  "sys1hip_linear_bf16", "sys1hip_pack_gated_weight", "sys1hip_query_kernel",
                  "sys1hip_set_kernel", "sys1hip_set_grid", "sys1hip_set_dp_tiles",
                  "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
-                 "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_kernel_count"):
+                 "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_kernel_count",
+                 "sys1hip_linear_bf16_noalloc"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

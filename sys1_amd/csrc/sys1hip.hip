@@ -89,6 +89,7 @@ struct Context {
   // Resident workgroups per CU of each (kernel, epilogue) as the runtime
   // reports them (an epilogue that needs more registers can fit fewer).
   std::vector<int> occ;
+  const int* occ_fixed = nullptr;  // the same table in static storage (the context-free entry point)
   // Chosen plans of unforced calls, keyed by shape and epilogue: pricing
   // every (kernel, grid) takes several microseconds of host time, more than
   // a small-M projection's kernel.
@@ -183,7 +184,8 @@ constexpr int64_t kLongK = 4096;            // see KernelEntry::long_k_efficienc
 constexpr double kProducerLatencyClk = 900.0;
 
 int occupancy(const Context* c, int id, int epi) {
-  const int n = c->occ.empty() ? 0 : c->occ[(size_t)id * kEpiCount + epi];
+  const int n = c->occ_fixed ? c->occ_fixed[(size_t)id * kEpiCount + epi]
+                : c->occ.empty() ? 0 : c->occ[(size_t)id * kEpiCount + epi];
   return n > 0 ? std::min(n, kKernels[id].occupancy) : kKernels[id].occupancy;
 }
 
@@ -432,6 +434,69 @@ int use_device(Context* c) {
   return SYS1HIP_OK;
 }
 
+// Argument checks of sys1hip_linear_bf16 (and its context-free variant).
+int check_linear(const char* who, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t ldw,
+                 const uint16_t* bias, const uint16_t* residual, int64_t ldr, uint16_t* y, int64_t ldy,
+                 int64_t M, int64_t N, int64_t K, int32_t epilogue) {
+  const int epi = epi_id_from_flags(epilogue);
+  if (epi < 0) return fail(SYS1HIP_EINVAL, "%s: unsupported epilogue flags %d", who, epilogue);
+  if (M < 0 || N <= 0 || K <= 0)
+    return fail(SYS1HIP_EINVAL, "%s: bad shape M=%lld N=%lld K=%lld", who, (long long)M, (long long)N,
+                (long long)K);
+  const bool gated = epi_gated(epi);
+  if (gated && (N % (2 * SYS1HIP_GATE_GROUP)) != 0)
+    return fail(SYS1HIP_EINVAL, "%s: gated epilogue needs N %% 32 == 0 (N=%lld)", who, (long long)N);
+  const int64_t nout = gated ? N / 2 : N;
+  if (M == 0) return SYS1HIP_OK;
+  if (!x || !w || !y) return fail(SYS1HIP_EINVAL, "%s: null x, w or y", who);
+  const bool want_bias = epilogue & SYS1HIP_EPI_BIAS;
+  const bool want_res = epilogue & SYS1HIP_EPI_RESIDUAL;
+  if (want_bias != (bias != nullptr))
+    return fail(SYS1HIP_EINVAL, "%s: bias pointer %s but epilogue flags %d", who, bias ? "given" : "missing",
+                epilogue);
+  if (want_res != (residual != nullptr))
+    return fail(SYS1HIP_EINVAL, "%s: residual pointer %s but epilogue flags %d", who,
+                residual ? "given" : "missing", epilogue);
+  if (ldx < K || ldw < K || ldy < nout || (want_res && ldr < nout))
+    return fail(SYS1HIP_EINVAL, "%s: leading dimension too small (ldx=%lld ldw=%lld ldy=%lld ldr=%lld)", who,
+                (long long)ldx, (long long)ldw, (long long)ldy, (long long)ldr);
+  if (K % 8 || ldx % 8 || ldw % 8) return fail(SYS1HIP_EALIGN, "%s: K, ldx and ldw must be multiples of 8", who);
+  if (!aligned16(x) || !aligned16(w)) return fail(SYS1HIP_EALIGN, "%s: x and w must be 16-byte aligned", who);
+  if (M > (1ll << 30) || N > (1ll << 30) || K > (1ll << 30))
+    return fail(SYS1HIP_ERANGE, "%s: dimension above 2^30", who);
+  return SYS1HIP_OK;
+}
+
+// Launch a checked projection on `plan` with the given stream-K workspace
+// (kWorkspaceBytes of partials, kCounterSlots arrival counters).
+int launch_linear(const char* who, const Context* c, const Plan& p, hipStream_t stream, float* ws,
+                  unsigned* counters, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t ldw,
+                  const uint16_t* bias, const uint16_t* residual, int64_t ldr, uint16_t* y, int64_t ldy,
+                  int64_t M, int64_t N, int64_t K, int epi) {
+  (void)c;
+  if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "%s: the forced kernel does not fit this call", who);
+  const KernelEntry& e = kKernels[p.kernel];
+  const int64_t grid = p.grid;
+  if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
+    return fail(SYS1HIP_ERANGE, "%s: more split tiles than stream-K counters", who);
+  GemmArgs a = {};
+  a.x = reinterpret_cast<const __bf16*>(x);
+  a.w = reinterpret_cast<const __bf16*>(w);
+  a.bias = reinterpret_cast<const __bf16*>(bias);
+  a.resid = reinterpret_cast<const __bf16*>(residual);
+  a.y = reinterpret_cast<__bf16*>(y);
+  a.ws = ws;
+  a.counters = counters;
+  a.ldx = ldx, a.ldw = ldw, a.ldr = ldr, a.ldy = ldy;
+  a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)(epi_gated(epi) ? N / 2 : N);
+  a.dp_tiles = (int)std::min<int64_t>(p.dp, 1 << 30);
+  a.group_m = raster_group(K);
+  if (grid <= 0 || grid > 0x7fffffff) return fail(SYS1HIP_ERANGE, "%s: grid of %lld workgroups", who, (long long)grid);
+  hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)grid), dim3(e.threads), 0, stream, a);
+  HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -589,64 +654,102 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
                         int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t epilogue) {
   if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: null context");
   Context* c = static_cast<Context*>(ctx);
-  const int epi = epi_id_from_flags(epilogue);
-  if (epi < 0) return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: unsupported epilogue flags %d", epilogue);
-  if (M < 0 || N <= 0 || K <= 0)
-    return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: bad shape M=%lld N=%lld K=%lld", (long long)M,
-                (long long)N, (long long)K);
-  const bool gated = epi_gated(epi);
-  if (gated && (N % (2 * SYS1HIP_GATE_GROUP)) != 0)
-    return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: gated epilogue needs N %% 32 == 0 (N=%lld)",
-                (long long)N);
-  const int64_t nout = gated ? N / 2 : N;
-  if (M == 0) return SYS1HIP_OK;
-  if (!x || !w || !y) return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: null x, w or y");
-  const bool want_bias = epilogue & SYS1HIP_EPI_BIAS;
-  const bool want_res = epilogue & SYS1HIP_EPI_RESIDUAL;
-  if (want_bias != (bias != nullptr))
-    return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: bias pointer %s but epilogue flags %d",
-                bias ? "given" : "missing", epilogue);
-  if (want_res != (residual != nullptr))
-    return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: residual pointer %s but epilogue flags %d",
-                residual ? "given" : "missing", epilogue);
-  if (ldx < K || ldw < K || ldy < nout || (want_res && ldr < nout))
-    return fail(SYS1HIP_EINVAL,
-                "sys1hip_linear_bf16: leading dimension too small (ldx=%lld ldw=%lld ldy=%lld ldr=%lld)",
-                (long long)ldx, (long long)ldw, (long long)ldy, (long long)ldr);
-  if (K % 8 || ldx % 8 || ldw % 8)
-    return fail(SYS1HIP_EALIGN, "sys1hip_linear_bf16: K, ldx and ldw must be multiples of 8");
-  if (!aligned16(x) || !aligned16(w))
-    return fail(SYS1HIP_EALIGN, "sys1hip_linear_bf16: x and w must be 16-byte aligned");
-  if (M > (1ll << 30) || N > (1ll << 30) || K > (1ll << 30))
-    return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: dimension above 2^30");
-
-  int rc = use_device(c);
+  int rc = check_linear("sys1hip_linear_bf16", x, ldx, w, ldw, bias, residual, ldr, y, ldy, M, N, K, epilogue);
+  if (rc || M == 0) return rc;
+  rc = use_device(c);
   if (rc) return rc;
-  const Plan p = resolve(c, M, N, K, ldw, epi);
-  if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_linear_bf16: the forced kernel does not fit this call");
-  const KernelEntry& e = kKernels[p.kernel];
-  const int64_t grid = p.grid;
-  if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
-    return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: more split tiles than stream-K counters");
+  const int epi = epi_id_from_flags(epilogue);
+  return launch_linear("sys1hip_linear_bf16", c, resolve(c, M, N, K, ldw, epi), c->stream, c->ws, c->counters, x,
+                       ldx, w, ldw, bias, residual, ldr, y, ldy, M, N, K, epi);
+}
 
-  GemmArgs a;
-  a.x = reinterpret_cast<const __bf16*>(x);
-  a.w = reinterpret_cast<const __bf16*>(w);
-  a.bias = reinterpret_cast<const __bf16*>(bias);
-  a.resid = reinterpret_cast<const __bf16*>(residual);
-  a.y = reinterpret_cast<__bf16*>(y);
-  a.ws = c->ws;
-  a.counters = c->counters;
-  a.ldx = ldx, a.ldw = ldw, a.ldr = ldr, a.ldy = ldy;
-  a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)nout;
-  a.dp_tiles = (int)std::min<int64_t>(p.dp, 1 << 30);
-  a.group_m = raster_group(K);
+}  // extern "C"
 
-  if (grid <= 0 || grid > 0x7fffffff)
-    return fail(SYS1HIP_ERANGE, "sys1hip_linear_bf16: grid of %lld workgroups", (long long)grid);
-  hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)grid), dim3(e.threads), 0, c->stream, a);
-  HIP_TRY(hipGetLastError());
+namespace {
+
+// ---- The context-free entry point that allocates nothing
+// (sys1hip_linear_bf16_noalloc).  Its stream-K workspace is `scratch`, a
+// static device array: each GPU the library runs on holds one copy, at its
+// own address, from the module's load to the end of the process.  Host code
+// must not use the array's name as a device address (it is a host-side
+// stand-in); each device's address comes from hipGetSymbolAddress, taken
+// once per device with that device current, and only that address is
+// passed to kernels.
+constexpr int kMaxStaticDevices = 64;
+constexpr size_t kScratchBytes = kWorkspaceBytes + (size_t)kCounterSlots * sizeof(unsigned);
+__device__ __align__(256) char scratch[kScratchBytes];
+
+__global__ void clear_words_kernel(unsigned* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Per device: the scratch address and the plan inputs (CU count and the
+// kernels' occupancy), all in static storage.
+struct StaticDevice {
+  std::once_flag once;
+  int rc = SYS1HIP_OK;
+  char* ptr = nullptr;
+  Context plan_ctx;  // only cus and occ_fixed are used (price_plans)
+  int occ[kNumKernels * kEpiCount] = {};
+};
+StaticDevice g_static[kMaxStaticDevices];
+
+int setup_static(StaticDevice& d, int dev, hipStream_t stream) {
+  HIP_TRY(hipGetSymbolAddress(reinterpret_cast<void**>(&d.ptr), HIP_SYMBOL(scratch)));
+  if (!d.ptr) return fail(SYS1HIP_EDEVICE, "sys1hip_linear_bf16_noalloc: no scratch address on device %d", dev);
+  int cus = 0;
+  HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  d.plan_ctx.cus = cus > 0 ? cus : 256;
+  for (int id = 0; id < kNumKernels; ++id)
+    for (int epi = 0; epi < kEpiCount; ++epi) {
+      int n = 0;
+      const KernelFn fn = kKernels[id].fn[epi];
+      if (fn && hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(fn),
+                                                             kKernels[id].threads, 0) == hipSuccess)
+        d.occ[id * kEpiCount + epi] = n;
+    }
+  (void)hipGetLastError();
+  d.plan_ctx.occ_fixed = d.occ;
+  // The arrival counters must start at zero (device globals are zeroed at
+  // load; each stream-K call's last arriving waves re-arm theirs).  When
+  // the first call is not being captured, they are also cleared explicitly,
+  // with a kernel on the caller's stream (ordered before the call).
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(stream, &st));
+  if (st == hipStreamCaptureStatusNone) {
+    hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)cdiv(kCounterSlots, 256)), dim3(256), 0, stream,
+                       reinterpret_cast<unsigned*>(d.ptr + kWorkspaceBytes), (int64_t)kCounterSlots);
+    HIP_TRY(hipGetLastError());
+  }
   return SYS1HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sys1hip_linear_bf16_noalloc(void* stream, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t ldw,
+                                const uint16_t* bias, const uint16_t* residual, int64_t ldr, uint16_t* y,
+                                int64_t ldy, int64_t M, int64_t N, int64_t K, int32_t epilogue) {
+  static const char* who = "sys1hip_linear_bf16_noalloc";
+  int rc = check_linear(who, x, ldx, w, ldw, bias, residual, ldr, y, ldy, M, N, K, epilogue);
+  if (rc || M == 0) return rc;
+  int dev = -1;
+  HIP_TRY(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxStaticDevices)
+    return fail(SYS1HIP_EDEVICE, "%s: device %d beyond the %d this entry point serves", who, dev, kMaxStaticDevices);
+  StaticDevice& d = g_static[dev];
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  std::call_once(d.once, [&] { d.rc = setup_static(d, dev, s); });
+  if (d.rc) return fail(d.rc, "%s: set-up on device %d failed", who, dev);
+  // The plan is priced on every call (no cache: a cache insert would
+  // allocate host memory).
+  const int epi = epi_id_from_flags(epilogue);
+  const Plan p = price_plans(&d.plan_ctx, M, N, K, ldw, epi, false, false);
+  return launch_linear(who, &d.plan_ctx, p, s, reinterpret_cast<float*>(d.ptr),
+                       reinterpret_cast<unsigned*>(d.ptr + kWorkspaceBytes), x, ldx, w, ldw, bias, residual, ldr,
+                       y, ldy, M, N, K, epi);
 }
 
 int sys1hip_linear_rope_qkv_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_t* w,

@@ -1,0 +1,68 @@
+"""The context-free, allocation-free entry point (sys1hip_linear_bf16_noalloc)
+through the C ABI: its output equals sys1hip_linear_bf16's on the same
+inputs (same kernel plan, so bit for bit), on two calls in a row, the second
+with a smaller input -- the static workspace keeps the first call's
+contents, and its arrival counters must come back re-armed."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from gpu_helpers import assert_parity, to_gpu_bf16, to_np
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _call(L, fn, first, x, w, y, bias=None, res=None, epi=0):
+    M, K = x.shape
+    N = w.shape[0]
+    rc = fn(first, _ptr(x), x.stride(0), _ptr(w), w.stride(0), _ptr(bias), _ptr(res),
+            res.stride(0) if res is not None else 0, _ptr(y), y.stride(0), M, N, K, epi)
+    return rc
+
+
+def test_noalloc_matches_the_context_entry_point(orc):
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from sys1_amd import _lib
+    from sys1_amd.device import HipDevice
+    L = _lib.load()
+    dev = HipDevice(0)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dev.follow_torch_stream()
+    # Two calls in a row, the second smaller: stream-K plans (weights above
+    # the skinny kernels' 32 MB, so the static workspace and its counters
+    # are used), then tile and skinny plans, with and without epilogues.
+    cases = [(96, 8192, 4096, 0), (48, 4096, 5120, 0), (40, 6144, 4096, _lib.EPI_RESIDUAL),
+             (600, 768, 768, _lib.EPI_RESIDUAL), (33, 3072, 1024, 0), (64, 4096, 2048, _lib.EPI_GEGLU)]
+    for (M, N, K, epi) in cases:
+        print(f"[gpu] noalloc M={M} N={N} K={K} epi={epi} plan={dev.query_kernel(M, N, K, epi)[1]}", flush=True)
+        x = to_gpu_bf16(orc.fill_normal((M, K), 3 + M), torch)
+        w = to_gpu_bf16(orc.fill_normal((N, K), 4 + N, 0.02), torch)
+        nout = N // 2 if epi == _lib.EPI_GEGLU else N
+        if epi == _lib.EPI_GEGLU:
+            wp = torch.empty_like(w)
+            _lib.check(L.sys1hip_pack_gated_weight(dev.ctx, _ptr(w), _ptr(wp), N, K), dev.ctx)
+            w = wp
+        res = to_gpu_bf16(orc.fill_normal((M, nout), 5), torch) if epi == _lib.EPI_RESIDUAL else None
+        y_ctx = torch.empty(M, nout, dtype=torch.bfloat16, device="cuda:0")
+        y_static = torch.full((M, nout), float("nan"), dtype=torch.bfloat16, device="cuda:0")
+        _lib.check(_call(L, L.sys1hip_linear_bf16, dev.ctx, x, w, y_ctx, res=res, epi=epi), dev.ctx)
+        _lib.check(_call(L, L.sys1hip_linear_bf16_noalloc, stream, x, w, y_static, res=res, epi=epi))
+        torch.cuda.synchronize()
+        assert torch.equal(y_ctx, y_static), f"M={M} N={N} K={K} epi={epi}"
+        if epi == 0:
+            assert_parity(to_np(y_static), orc.linear_f32(to_np(x), to_np(w)), f"noalloc M={M} N={N} K={K}")
+    # the refused call: a bad shape reports an error, not a launch
+    x = to_gpu_bf16(orc.fill_normal((8, 64), 1), torch)
+    w = to_gpu_bf16(orc.fill_normal((64, 64), 2), torch)
+    y = torch.empty(8, 64, dtype=torch.bfloat16, device="cuda:0")
+    rc = L.sys1hip_linear_bf16_noalloc(stream, _ptr(x), 64, _ptr(w), 64, None, None, 0, _ptr(y), 64,
+                                       8, 64, 60, 0)
+    assert rc == _lib.EALIGN
