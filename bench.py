@@ -53,6 +53,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--no-small-m", action="store_true",
+                    help="skip the small-M (ModernBERT-large at M = 64 and 256) object of the line")
     ap.add_argument("--norms", action="store_true",
                     help="fuse each projection's pre-norm (LayerNorm / RMSNorm) into it; the "
                          "row-statistics pass then sits inside the timed step")
@@ -141,6 +143,84 @@ def cpu_baseline(seconds: float) -> dict:
                       f"M=1024 (8x128), {layers} layers in {el:.1f} s; "
                       f"{layers * M / el:.0f} layer-tokens/s = {layers * M / el / 22:.0f} "
                       f"22-layer tokens/s"}
+
+
+def small_m_pass(dev, seed: int, steps: int = 20) -> dict:
+    """BASELINE config 3 at the skinny end: the ModernBERT-large projection
+    stack (28 layers, hidden 1024, GeGLU 2x2624) at M = 64 and M = 256
+    packed tokens.  Per projection: the kernel the plan picks, its average
+    time from HIP events around each launch (each step queued behind a spin
+    kernel longer than the host's enqueue, so the events bracket the GPU
+    work; they include the launch's dispatch gap, so they run a little above
+    rocprofv3's kernel durations), the algorithmic HBM bytes per launch and
+    their rate as a fraction of the 8 TB/s peak."""
+    import numpy as np
+    import torch
+    from sys1_amd.stacks import CONFIGS, ProjectionStack
+    cfg = CONFIGS["modernbert-large"]()
+    stack = ProjectionStack(cfg, dev, 256, seed=seed)
+    gen = torch.Generator(device="cuda:0")
+    gen.manual_seed(seed + 2000)
+    x = torch.randn(256, cfg.hidden, generator=gen, device="cuda:0").to(torch.bfloat16)
+    out = {}
+    for M in (64, 256):
+        prep = stack.prepare(x, M)
+        for _ in range(3):
+            stack.run_prepared(prep)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            stack.run_prepared(prep)
+        t1.record()
+        torch.cuda.synchronize()
+        step_ms = t0.elapsed_time(t1) / steps
+        tq = time.perf_counter()
+        stack.run_prepared(prep)
+        host_s = time.perf_counter() - tq
+        torch.cuda.synchronize()
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record()
+        torch.cuda._sleep(1 << 20)
+        c1.record()
+        torch.cuda.synchronize()
+        spin = int((1 << 20) * 2.0 * host_s / (c0.elapsed_time(c1) * 1e-3)) + 1
+        recs = []
+        for _ in range(steps):
+            torch.cuda._sleep(spin)
+            for p, fn, a in prep:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                if fn(*a):
+                    raise RuntimeError("launch failed")
+                e1.record()
+                recs.append((p, e0, e1))
+        torch.cuda.synchronize()
+        per = {}
+        for p, e0, e1 in recs:
+            d = per.setdefault(p.name, {"ms": 0.0, "n": 0, "bytes": p.bytes(M), "N": p.N, "K": p.K,
+                                        "epi": p.epi})
+            d["ms"] += e0.elapsed_time(e1)
+            d["n"] += 1
+        res = {}
+        for name, d in per.items():
+            us = d["ms"] / d["n"] * 1e3
+            gbs = d["bytes"] / (us * 1e-6) / 1e9
+            res[name] = {"kernel": dev.query_kernel(M, d["N"], d["K"], d["epi"])[1], "avg_us": round(us, 2),
+                         "bytes": d["bytes"], "gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        dom = max(res, key=lambda k: res[k]["avg_us"])
+        total_bytes = sum(p.bytes(M) for layer in cfg.layers for p in layer)
+        out[f"M{M}"] = {
+            "step_ms": round(step_ms, 4),
+            "stack_gbs": round(total_bytes / (step_ms * 1e-3) / 1e9, 1),
+            "stack_frac": round(total_bytes / (step_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "tflops": round(cfg.flops_per_token() * M / (step_ms * 1e-3) / 1e12, 2),
+            "dominant": {"projection": dom, **res[dom]},
+            "per_projection": res,
+        }
+    out["note"] = ("ModernBERT-large (config 3) projection stack, 28 layers; per-projection times from "
+                   "HIP events (include the dispatch gap); bytes are algorithmic per launch")
+    return out
 
 
 def main():
@@ -325,6 +405,10 @@ def main():
             torch.neg(src, out=dst)
         torch.cuda.synchronize()
 
+    small_m = None
+    if not args.no_small_m and args.workload == "modernbert-base" and not args.tokens:
+        small_m = small_m_pass(dev, args.seed)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_seconds)
@@ -356,6 +440,7 @@ def main():
         "wall_s_timed": round(wall, 4),
         "roofline": roofline,
         "per_projection": per_proj,
+        "small_m": small_m,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

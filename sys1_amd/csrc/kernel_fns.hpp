@@ -52,11 +52,11 @@ constexpr KernelFn conv_fn() {
 #ifdef SYS1_SKINNY_HPP
 namespace sys1 {
 // A skinny-M kernel per epilogue; null where the epilogue does not apply
-// (gated epilogues need two 16-row blocks; RoPE and conv run on the tile
-// kernels).
+// (gated epilogues need whole 32-row gate/up groups, an even FN; RoPE and
+// conv run on the tile kernels).
 template <int FM, int FN, int NW, int U, int EPI>
 constexpr KernelFn skinny_fn() {
-  if constexpr ((epi_gated(EPI) && FN != 2) || epi_base(EPI) == kEpiRopeQkv || epi_base(EPI) == kEpiConvSilu)
+  if constexpr ((epi_gated(EPI) && FN % 2 != 0) || epi_base(EPI) == kEpiRopeQkv || epi_base(EPI) == kEpiConvSilu)
     return nullptr;
   else
     return skinny_kernel<FM, FN, NW, U, EPI>;

@@ -1,12 +1,13 @@
 // Skinny-M projection for gfx950: y[M,N] = epi(x[M,K] . w[N,K]^T) for a
-// few packed tokens (M <= 16 * FM <= 128), on v_mfma_f32_16x16x32_bf16.
+// few hundred packed tokens at most, on v_mfma_f32_16x16x32_bf16.
 //
 // The small-M regime is a weight stream: every weight byte is read once and
 // used for M outputs.  Up to ~32 MB of weight the stream is short next to
 // the latency of a memory round trip, so this kernel is built to need as
 // few dependent round trips as possible and no cross-workgroup fix-up:
-//   - workgroup b owns output columns [16 FN b, 16 FN (b + 1)) for all M
-//     rows, over the whole K;
+//   - workgroup b owns one BM x BN output tile (BM = 16 FM rows, BN = 16 FN
+//     columns; tile rows vary fastest over b, so neighbouring workgroups
+//     share their weight rows) over the whole K;
 //   - its NW waves split K into equal contiguous ranges of 32-wide k-steps
 //     and each loads its weight and activation fragments straight from
 //     memory into registers (no LDS staging), U k-steps per load group,
@@ -20,9 +21,9 @@
 // block is B (the same layout over token rows).  The 16x16 result block
 // holds, in lane l, register e: feature 4 (l / 16) + e of token l % 16.
 //
-// Gated epilogues (GeGLU / SwiGLU) need FN = 2: the packed gate/up layout
-// puts 16 gate rows and then the 16 matching up rows in each 32-row group,
-// which is exactly the workgroup's two 16-row blocks.
+// Gated epilogues (GeGLU / SwiGLU) need an even FN: the packed gate/up
+// layout puts 16 gate rows and then the 16 matching up rows in each 32-row
+// group, i.e. in the workgroup's blocks 2g and 2g + 1.
 #pragma once
 #define SYS1_SKINNY_HPP
 
@@ -51,13 +52,15 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
   constexpr int E = epi_base(EPI);
   constexpr int NORM = epi_norm(EPI);
   constexpr bool kGated = epi_gated(E);
-  static_assert(!kGated || FN == 2, "gated epilogues: one 32-row gate/up group per workgroup");
+  static_assert(!kGated || FN % 2 == 0, "gated epilogues: whole 32-row gate/up groups per workgroup");
   static_assert(E != kEpiRopeQkv && E != kEpiConvSilu, "RoPE and conv epilogues run on the tile kernels");
   __shared__ __attribute__((aligned(16))) float red[NW * BM * S::kRowF32];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n0 = blockIdx.x * BN;
+  const int tiles_m = (a.M + BM - 1) / BM;
+  const int m0 = (int)(blockIdx.x % tiles_m) * BM;
+  const int n0 = (int)(blockIdx.x / tiles_m) * BN;
   const int r16 = lane & 15, q = lane >> 4;
   const int ksteps = (a.K + 31) / 32;
   const int s0 = wave * ksteps / NW, s1 = (wave + 1) * ksteps / NW;
@@ -67,7 +70,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
   // or N read the last row: computed, never stored).
   unsigned xo[FM], wo[FN];
 #pragma unroll
-  for (int j = 0; j < FM; ++j) xo[j] = (unsigned)((int64_t)min(j * 16 + r16, a.M - 1) * a.ldx * 2 + q * 16);
+  for (int j = 0; j < FM; ++j) xo[j] = (unsigned)((int64_t)min(m0 + j * 16 + r16, a.M - 1) * a.ldx * 2 + q * 16);
 #pragma unroll
   for (int i = 0; i < FN; ++i) wo[i] = (unsigned)((int64_t)min(n0 + i * 16 + r16, a.N - 1) * a.ldw * 2 + q * 16);
 
@@ -132,9 +135,13 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
   constexpr int kVecs = kOutCols / 8;
   const int out_n0 = kGated ? n0 / 2 : n0;
   for (int t = threadIdx.x; t < BM * kVecs; t += NW * 64) {
-    const int m = t / kVecs, c0 = (t % kVecs) * 8;
+    const int r = t / kVecs, c0 = (t % kVecs) * 8;
+    const int m = m0 + r;
     if (m >= a.M) continue;
     const int n = out_n0 + c0;
+    // partial-slab column of the output column (gated: the gate block of
+    // its 32-row group; the up block is 16 columns further)
+    const int pc = kGated ? (c0 / 16) * 32 + c0 % 16 : c0;
     if (n >= a.Nout) continue;
     const int valid = a.Nout - n;
     float v[8], g[8];
@@ -142,17 +149,17 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
     for (int e = 0; e < 8; ++e) v[e] = g[e] = 0.0f;
 #pragma unroll 4
     for (int ww = 0; ww < NW; ++ww) {
-      const float* row = red + (ww * BM + m) * S::kRowF32;
-      const f32x4 p0 = *reinterpret_cast<const f32x4*>(row + c0);
-      const f32x4 p1 = *reinterpret_cast<const f32x4*>(row + c0 + 4);
+      const float* row = red + (ww * BM + r) * S::kRowF32;
+      const f32x4 p0 = *reinterpret_cast<const f32x4*>(row + pc);
+      const f32x4 p1 = *reinterpret_cast<const f32x4*>(row + pc + 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         v[e] += p0[e];
         v[4 + e] += p1[e];
       }
       if constexpr (kGated) {  // the up rows of the same columns, 16 rows further
-        const f32x4 u0 = *reinterpret_cast<const f32x4*>(row + 16 + c0);
-        const f32x4 u1 = *reinterpret_cast<const f32x4*>(row + 16 + c0 + 4);
+        const f32x4 u0 = *reinterpret_cast<const f32x4*>(row + pc + 16);
+        const f32x4 u1 = *reinterpret_cast<const f32x4*>(row + pc + 20);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           g[e] += u0[e];
@@ -167,7 +174,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if constexpr (NORM == kNormLayer) {
-          const int wn = min(n0 + c0 + e, a.N - 1);  // weight row of the gate (or plain) column
+          const int wn = min(n0 + pc + e, a.N - 1);  // weight row of the gate (or plain) column
           v[e] = r * (v[e] - mu * a.colsum[wn]);
           if constexpr (kGated) g[e] = r * (g[e] - mu * a.colsum[min(wn + 16, a.N - 1)]);
         } else {

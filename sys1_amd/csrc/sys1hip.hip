@@ -112,7 +112,7 @@ struct KernelEntry {
   float swiglu_efficiency;  // efficiency with a SwiGLU epilogue, when it differs (0: the same)
   float long_k_efficiency;  // efficiency for K > kLongK, when it differs (0: the same)
   const KernelFn* fn;   // [kEpiCount]: the shape's kernel per epilogue (null: not built)
-  bool skinny;          // skinny-M kernel (skinny.hpp): one workgroup per bn columns, all rows
+  bool skinny;          // skinny-M kernel (skinny.hpp): one workgroup per bm x bn tile, whole K
 };
 
 }  // namespace
@@ -240,7 +240,7 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
 
 int64_t max_grid(const Context* c, int id, int epi, int64_t M, int64_t N, int64_t K) {
   const KernelEntry& e = kKernels[id];
-  if (e.skinny) return cdiv(N, e.bn);  // one workgroup per bn columns
+  if (e.skinny) return cdiv(M, e.bm) * cdiv(N, e.bn);  // one workgroup per tile
   const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
   int64_t g = (int64_t)c->cus * occupancy(c, id, epi);
   if (!e.streamk) return std::min(g, tiles);
@@ -293,43 +293,44 @@ int64_t halo_rows(const KernelEntry& e, int64_t M, int halo) {
 constexpr int64_t kCachedWeightBytes = 32 << 20;
 constexpr int64_t kRereadWeightBytes = 128 << 20;  // half the 256 MB MALL
 
-// The skinny-M kernel for a call, or -1.  Each skinny workgroup reads its
-// bn weight rows and all of x over the whole K, so a CU moves
-//   ceil(workgroups / CUs) * (rows + bn) * K * 2 bytes
-// through its load path; the kernel wins while that stays within
-// kSkinnyCuBytes (measured over the ModernBERT-base/large and Qwen3.5-small
-// projections at M = 16..128: 295-420 KB per CU ran 1.1-1.7x faster than
-// the stream-K kernels, 590-655 KB tied, 756 KB and above lost).  Above
-// kSkinnyWeightBytes the weight is streamed from HBM and needs the
-// stream-K schedule's spread of K over every CU.  The rows are the smallest
-// 16 FM >= M; non-gated calls take the 16- or 32-column shape that moves
-// fewer bytes per CU (16 on a tie: more workgroups in flight), gated calls
-// the 32-column one (one gate/up row group per workgroup).
-constexpr int64_t kSkinnyMaxM = 128;
+// The skinny-M kernel for a call, or -1.  A skinny workgroup reads its BN
+// weight rows and its BM rows of x over the whole K, so the busiest CU
+// moves
+//   ceil(tiles / CUs) * (BM + BN) * K * 2 bytes
+// through its load path; the shape with the fewest such bytes is taken
+// (ties: the first listed), and the skinny kernels win while that stays
+// within kSkinnyCuBytes (measured over the ModernBERT-base/large and
+// Qwen3.5-small projections at M = 16..256: up to ~420 KB per CU ran
+// 1.1-1.7x faster than the stream-K and tile kernels, ~600 KB tied, more
+// lost).  Above kSkinnyWeightBytes the weight is streamed from HBM and
+// needs the stream-K schedule's spread of K over every CU.
+constexpr int64_t kSkinnyMaxM = 512;
 constexpr int64_t kSkinnyWeightBytes = 32 << 20;
 constexpr int64_t kSkinnyCuBytes = 512 << 10;
 
 int skinny_pick(const Context* c, int64_t M, int64_t N, int64_t K, int64_t ldw, int epi) {
   if (M > kSkinnyMaxM || 2 * N * K > kSkinnyWeightBytes || 2 * N * ldw >= 0x7ffffff0ll) return -1;
-  const int64_t bm = M <= 16 ? 16 : M <= 32 ? 32 : M <= 64 ? 64 : 128;
-  auto cu_bytes = [&](int64_t bn) { return cdiv(cdiv(N, bn), c->cus) * (bm + bn) * K * 2; };
-  int64_t bn = 32;
-  if (!epi_gated(epi) && cu_bytes(16) <= cu_bytes(32)) bn = 16;
-  if (cu_bytes(bn) > kSkinnyCuBytes) return -1;
+  int best = -1;
+  int64_t best_bytes = 0;
   for (int id = 0; id < kNumKernels; ++id) {
     const KernelEntry& e = kKernels[id];
-    if (e.skinny && e.bm == bm && e.bn == bn && e.fn[epi]) return id;
+    if (!e.skinny || !e.fn[epi]) continue;
+    const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
+    const int64_t bytes = cdiv(tiles, c->cus) * (e.bm + e.bn) * K * 2;
+    if (best < 0 || bytes < best_bytes) best = id, best_bytes = bytes;
   }
-  return -1;
+  return best >= 0 && best_bytes <= kSkinnyCuBytes ? best : -1;
 }
 
 Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int64_t ldw, int epi, bool head64,
                  bool conv) {
   Plan best;
-  if (c->forced_kernel < 0 && !head64 && !conv) {
+  // (a forced grid or split asks for a persistent kernel: no skinny pick)
+  if (c->forced_kernel < 0 && c->forced_grid <= 0 && c->forced_dp < 0 && !head64 && !conv) {
     const int id = skinny_pick(c, M0, N, K, ldw, epi);
     if (id >= 0) {
-      best.kernel = id, best.grid = cdiv(N, kKernels[id].bn), best.dp = 0, best.cost = 0.0;
+      best.kernel = id, best.grid = cdiv(M0, kKernels[id].bm) * cdiv(N, kKernels[id].bn), best.dp = 0,
+      best.cost = 0.0;
       return best;
     }
   }
@@ -338,9 +339,10 @@ Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int64_t ldw
     const KernelEntry& e = kKernels[id];
     if (!e.fn[epi]) continue;
     if (e.skinny) {
-      // (only when forced: the automatic choice is skinny_pick's)
-      if (c->forced_kernel != id || M0 > e.bm || head64 || conv || 2 * N * ldw >= 0x7ffffff0ll) continue;
-      best.kernel = id, best.grid = cdiv(N, e.bn), best.dp = 0, best.cost = 0.0;
+      // (only when forced: the automatic choice is skinny_pick's; the grid
+      // is one workgroup per tile, whatever grid is forced)
+      if (c->forced_kernel != id || head64 || conv || 2 * N * ldw >= 0x7ffffff0ll) continue;
+      best.kernel = id, best.grid = cdiv(M0, e.bm) * cdiv(N, e.bn), best.dp = 0, best.cost = 0.0;
       continue;
     }
     if (head64 && e.tn != 64) continue;

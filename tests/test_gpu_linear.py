@@ -77,13 +77,13 @@ def test_every_kernel_every_epilogue(dev, orc, kid, name):
     if name.startswith("stream_"):
         cap = int(name.split("_")[1].split("x")[0])
         Ms = sorted({max(1, cap // 2 + 3), cap, 300})
-    elif skinny:  # M up to the kernel's rows (a forced skinny kernel refuses more)
+    elif skinny:  # one tile row, and several with a ragged last one
         cap = int(name.split("_")[1].split("x")[0])
-        Ms = sorted({1, max(1, cap // 2 + 3), cap})
+        Ms = sorted({1, max(1, cap // 2 + 3), cap, 300})
     else:
         Ms = [300, 513]
-    # (a two-block skinny kernel is the one that runs the gated epilogues)
-    gated_ok = not skinny or name.split("_")[1].endswith("x32")
+    # (skinny kernels with whole 32-row gate/up groups run the gated epilogues)
+    gated_ok = not skinny or int(name.split("_")[1].split("x")[1]) % 32 == 0
     dev.set_kernel(kid)
     try:
         for M in Ms:
@@ -453,18 +453,19 @@ def test_python_errors(dev, orc):
                                    if n.startswith("skinny_")])
 def test_skinny_kernels_ragged_shapes(dev, orc, kname):
     """The skinny-M kernels: K split over the waves with empty, one-step and
-    tail (K % 32 != 0) ranges, N not a multiple of the 16-column block (the
-    last workgroup's rows clamped, its columns stored element by element),
-    every M up to the kernel's rows, and repeated calls bit-identical (the
-    waves' partials are summed in a fixed order)."""
+    tail (K % 32 != 0) ranges, N not a multiple of the tile width (the last
+    tile's weight rows clamped, its columns stored element by element), M
+    within one tile row and over several with a ragged last one, and
+    repeated calls bit-identical (the waves' partials are summed in a fixed
+    order)."""
     from sys1_amd import kernel_names
     from sys1_amd.linear import GatedLinear, Linear
     cap = int(kname.split("_")[1].split("x")[0])
-    two_block = kname.split("_")[1].endswith("x32")
+    gated = int(kname.split("_")[1].split("x")[1]) % 32 == 0
     dev.set_kernel(kernel_names().index(kname))
     try:
         for (M, N, K) in [(1, 1, 40), (cap, 17, 72), (max(1, cap - 5), 520, 136), (cap, 1000, 1000),
-                          (min(cap, 7), 48, 4104), (cap, 64, 8)]:
+                          (min(cap, 7), 48, 4104), (cap, 64, 8), (2 * cap + 5, 200, 328)]:
             print(f"[gpu] {kname} M={M} N={N} K={K}", flush=True)
             x, w = _inputs(orc, M, N, K, 91 + M + K)
             proj = orc.linear_f64(orc.round_bf16(x), orc.round_bf16(w)).astype(np.float32)
@@ -473,17 +474,12 @@ def test_skinny_kernels_ragged_shapes(dev, orc, kname):
             y = to_np(lin(xg))
             _check_close_to_rounded(orc, y, proj, f"{kname} M={M} N={N} K={K}")
             np.testing.assert_array_equal(y, to_np(lin(xg)))
-            if two_block and N % 32 == 0:
+            if gated and N % 32 == 0:
                 p16 = orc.round_bf16(proj)
                 I = N // 2
                 ref = orc.round_bf16(orc.round_bf16(orc.silu(p16[:, :I])) * p16[:, I:])
                 assert_parity(to_np(GatedLinear(to_gpu_bf16(w, torch), "silu", device=dev)(xg)), ref,
                               f"{kname} swiglu M={M} N={N} K={K}")
-        # more rows than the kernel holds: the forced call is refused, not run
-        from sys1_amd import _lib
-        x, w = _inputs(orc, cap + 1, 64, 64, 5)
-        with pytest.raises(_lib.Sys1HipError):
-            Linear(to_gpu_bf16(w, torch), device=dev)(to_gpu_bf16(x, torch))
     finally:
         dev.set_kernel(-1)
 
