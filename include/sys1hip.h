@@ -59,6 +59,11 @@ extern "C" {
 #define SYS1HIP_EPI_SWIGLU 4   /* y = bf16(bf16(silu(g)) * u)         qwen35_text.rs:239     */
 #define SYS1HIP_EPI_RESIDUAL 8 /* y = bf16(bf16(...) + r)             modernbert.rs:883,886  */
 #define SYS1HIP_EPI_GELU 16    /* y = bf16(gelu_erf(bf16(... + b)))   laya.rs:513-515        */
+/* Not an epilogue: the weight argument is in the blocked layout of
+ * sys1hip_pack_blocked_weight (ldw is then unused).  Accepted by
+ * sys1hip_linear_bf16, sys1hip_linear_bf16_noalloc and
+ * sys1hip_norm_linear_bf16. */
+#define SYS1HIP_EPI_BLOCKED_W 32
 
 /* Packing granularity of gated weights: rows are interleaved in groups of
  * this many gate rows followed by as many up rows. */
@@ -245,6 +250,20 @@ SYS1HIP_API int sys1hip_linear_bf16_noalloc(void* stream,
                         uint16_t* y, int64_t ldy,
                         int64_t M, int64_t N, int64_t K,
                         int32_t epilogue);
+
+/* The blocked weight layout, a load-time repacking with no counterpart in
+ * the reference (whose weights stay [out,in] row-major): [N, K] bf16 as
+ * 32-row x 64-column blocks of 4 KB, row-major inside a block, blocks
+ * ordered by row block then k block, rows and K zero-padded.  One k-step of
+ * 32 weight rows is then 4 KB of contiguous memory instead of 32 pieces of
+ * 128 bytes, which is what the weight-streaming (small-M) kernels read.
+ * Packs w [N, ldw] (row-major; a gated weight after
+ * sys1hip_pack_gated_weight) into `packed`, which holds
+ * sys1hip_blocked_weight_bytes(N, K) bytes.  Returns that size, or -1 for a
+ * bad shape. */
+SYS1HIP_API int64_t sys1hip_blocked_weight_bytes(int64_t N, int64_t K);
+SYS1HIP_API int sys1hip_pack_blocked_weight(void* ctx, const uint16_t* w, int64_t ldw, uint16_t* packed,
+                                            int64_t N, int64_t K);
 
 /* Number of kernel ids and the name of one id (for sweeps). */
 SYS1HIP_API int sys1hip_kernel_count(void);

@@ -18,6 +18,7 @@ EPI_GEGLU = 2
 EPI_SWIGLU = 4
 EPI_RESIDUAL = 8
 EPI_GELU = 16
+EPI_BLOCKED_W = 32   # not an epilogue: the weight is in the blocked layout
 GATE_GROUP = 16
 
 # Pre-norm kinds (include/sys1hip.h).
@@ -38,6 +39,7 @@ EXPORTS = (
     "sys1hip_kernel_count", "sys1hip_kernel_name", "sys1hip_set_grid",
     "sys1hip_set_dp_tiles", "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
     "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_linear_bf16_noalloc",
+    "sys1hip_blocked_weight_bytes", "sys1hip_pack_blocked_weight",
 )
 
 
@@ -74,6 +76,9 @@ def load() -> ctypes.CDLL:
     L.sys1hip_linear_bf16_noalloc.argtypes = [vp, vp, i64, vp, i64, vp, vp, i64, vp, i64, i64, i64, i64,
                                               i32]
     L.sys1hip_pack_gated_weight.argtypes = [vp, vp, vp, i64, i64]
+    L.sys1hip_blocked_weight_bytes.argtypes = [i64, i64]
+    L.sys1hip_blocked_weight_bytes.restype = i64
+    L.sys1hip_pack_blocked_weight.argtypes = [vp, vp, i64, vp, i64, i64]
     L.sys1hip_query_kernel.argtypes = [vp, i64, i64, i64, i32, ctypes.c_char_p, i64]
     L.sys1hip_set_kernel.argtypes = [vp, i32]
     L.sys1hip_set_grid.argtypes = [vp, i32]
@@ -92,7 +97,7 @@ def load() -> ctypes.CDLL:
                  "sys1hip_set_kernel", "sys1hip_set_grid", "sys1hip_set_dp_tiles",
                  "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
                  "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_kernel_count",
-                 "sys1hip_linear_bf16_noalloc"):
+                 "sys1hip_linear_bf16_noalloc", "sys1hip_pack_blocked_weight"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

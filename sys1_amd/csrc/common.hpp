@@ -220,7 +220,17 @@ struct GemmArgs {
   // token m's position in its sequence.
   const __bf16* conv_w;
   int conv_ch;
+  // Weight layout.  0: row-major [N, ldw].  > 0: the blocked layout of
+  // sys1hip_pack_blocked_weight with this many 64-wide k-tiles per row
+  // block: 32-row x 64-k blocks of 4 KB, row-major inside, ordered
+  // [N / 32][w_kt] (rows and K zero-padded), so one k-tile of a 32-row block
+  // is 4 KB of contiguous memory.
+  int w_kt;
 };
+
+constexpr int kBlkRows = 32;                  // rows of a weight block
+constexpr int kBlkK = 64;                     // k values of a weight block
+constexpr int kBlkBytes = kBlkRows * kBlkK * 2;  // 4 KB
 
 // Map the hardware workgroup id to a logical tile id so that each XCD gets a
 // contiguous range of logical tiles.  Workgroups are dispatched round-robin

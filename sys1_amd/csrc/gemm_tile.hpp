@@ -71,6 +71,8 @@ __device__ __forceinline__ int lds_swz(int row) {
 
 template <int BM, int BN, int WM, int WN, int STAGES, int BK_>
 struct TileShape {
+  // (a blocked weight's k-tile is one 4 KB block per 32 tile rows)
+  static_assert(BN % kBlkRows == 0 && BK_ == kBlkK, "tiles start on weight blocks of the blocked layout");
   static constexpr int kWaves = WM * WN;
   static constexpr int kThreads = kWaves * 64;
   static constexpr int BK = BK_;
@@ -287,8 +289,10 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
     for (int i = 0; i < kDma; ++i) {
       const int r = dma_row(i);
       const int c = lpos ^ lds_swz<BK>(r);
+      const int rw = min(r, w_left);  // (tile rows start on a 32-row block: BN % 32 == 0)
       src_off[i] = i < kXDma ? (unsigned)(min(r, x_left) * (int)a.ldx * 2 + c * 16)
-                             : (unsigned)(min(r, w_left) * (int)a.ldw * 2 + c * 16);
+                   : a.w_kt ? (unsigned)((rw / kBlkRows) * a.w_kt * kBlkBytes + (rw % kBlkRows) * (kBlkK * 2) + c * 16)
+                            : (unsigned)(rw * (int)a.ldw * 2 + c * 16);
     }
   };
   Segment isg = walk.first_segment();
@@ -312,7 +316,10 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
     const int bytes = live ? 0x7ffffff0 : 0;
     r.base = lds + stage * S::kStageBytes;
     r.xr = make_rsrc_uniform(reinterpret_cast<const char*>(a.x + (int64_t)m0 * a.ldx) + is_kt * BK * 2, bytes);
-    r.wr = make_rsrc_uniform(reinterpret_cast<const char*>(a.w + (int64_t)n0 * a.ldw) + is_kt * BK * 2, bytes);
+    r.wr = make_rsrc_uniform(
+        a.w_kt ? reinterpret_cast<const char*>(a.w) + ((int64_t)(n0 / kBlkRows) * a.w_kt + is_kt) * kBlkBytes
+               : reinterpret_cast<const char*>(a.w + (int64_t)n0 * a.ldw) + is_kt * BK * 2,
+        bytes);
     r.kleft = a.K - is_kt * BK;
     return r;
   };

@@ -72,7 +72,14 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
 #pragma unroll
   for (int j = 0; j < FM; ++j) xo[j] = (unsigned)((int64_t)min(m0 + j * 16 + r16, a.M - 1) * a.ldx * 2 + q * 16);
 #pragma unroll
-  for (int i = 0; i < FN; ++i) wo[i] = (unsigned)((int64_t)min(n0 + i * 16 + r16, a.N - 1) * a.ldw * 2 + q * 16);
+  for (int i = 0; i < FN; ++i) {
+    const int n = min(n0 + i * 16 + r16, a.N - 1);
+    wo[i] = a.w_kt ? (unsigned)((n / kBlkRows) * a.w_kt * kBlkBytes + (n % kBlkRows) * (kBlkK * 2) + q * 16)
+                   : (unsigned)((int64_t)n * a.ldw * 2 + q * 16);
+  }
+  // Byte offset of k-step st (32 k values) from k = 0: 64 bytes of a
+  // row-major weight row, or for the blocked layout half of a 4 KB block.
+  auto wstep = [&](int st) { return a.w_kt ? (st >> 1) * kBlkBytes + (st & 1) * 64 : st * 64; };
 
   f32x4 acc[FN][FM];
 #pragma unroll
@@ -89,10 +96,12 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
     for (int u = 0; u < U; ++u) {
       const int st = s + u;
       const bool ok = st < s1 && st * 32 + q * 8 < a.K;
-      const int so = __builtin_amdgcn_readfirstlane(min(st, s1 - 1) * 64);
+      const int sc = min(st, s1 - 1);
+      const int so = __builtin_amdgcn_readfirstlane(sc * 64);
+      const int sw = __builtin_amdgcn_readfirstlane(wstep(sc));
 #pragma unroll
       for (int i = 0; i < FN; ++i)
-        bw[b][u][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, ok ? (int)wo[i] : (int)kOutOfRange, so, 0);
+        bw[b][u][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, ok ? (int)wo[i] : (int)kOutOfRange, sw, 0);
 #pragma unroll
       for (int j = 0; j < FM; ++j)
         bx[b][u][j] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? (int)xo[j] : (int)kOutOfRange, so, 0);

@@ -139,8 +139,9 @@ const KernelEntry kKernels[] = {
 };
 constexpr int kNumKernels = sizeof(kKernels) / sizeof(kKernels[0]);
 
+// (the weight-layout bit SYS1HIP_EPI_BLOCKED_W is not an epilogue)
 int epi_id_from_flags(int32_t f) {
-  switch (f) {
+  switch (f & ~SYS1HIP_EPI_BLOCKED_W) {
     case SYS1HIP_EPI_NONE: return kEpiNone;
     case SYS1HIP_EPI_BIAS: return kEpiBias;
     case SYS1HIP_EPI_GEGLU: return kEpiGeglu;
@@ -415,6 +416,23 @@ int raster_group(int64_t K) { return K > 8192 ? 4 : 3; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Bytes of a weight [N, K] in the blocked layout (see GemmArgs::w_kt).
+int64_t blocked_bytes(int64_t N, int64_t K) { return cdiv(N, kBlkRows) * cdiv(K, kBlkK) * kBlkBytes; }
+
+// Row-major [N, ldw] -> blocked layout, 16 bytes per thread; rows past N
+// and k past K are zeros.
+__global__ void pack_blocked_kernel(const __bf16* __restrict__ w, int64_t ldw, i32x4* __restrict__ out, int64_t N,
+                                    int64_t K, int64_t kt_count, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 16-byte unit of the output
+  if (idx >= total) return;
+  const int64_t blk = idx / (kBlkBytes / 16), in = idx % (kBlkBytes / 16);
+  const int64_t rb = blk / kt_count, kt = blk % kt_count;
+  const int64_t n = rb * kBlkRows + in / (kBlkK / 8), k = kt * kBlkK + (in % (kBlkK / 8)) * 8;
+  i32x4 v = {0, 0, 0, 0};
+  if (n < N && k < K) v = *reinterpret_cast<const i32x4*>(w + n * ldw + k);  // (K % 8 == 0: whole chunks)
+  out[idx] = v;
+}
+
 __global__ void pack_gated_kernel(const i32x4* __restrict__ w, i32x4* __restrict__ out,
                                   int64_t N, int64_t kv) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -459,14 +477,24 @@ int check_linear(const char* who, const uint16_t* x, int64_t ldx, const uint16_t
   if (want_res != (residual != nullptr))
     return fail(SYS1HIP_EINVAL, "%s: residual pointer %s but epilogue flags %d", who,
                 residual ? "given" : "missing", epilogue);
-  if (ldx < K || ldw < K || ldy < nout || (want_res && ldr < nout))
+  const bool blocked = epilogue & SYS1HIP_EPI_BLOCKED_W;  // (ldw unused: the blocked layout has none)
+  if (ldx < K || (!blocked && ldw < K) || ldy < nout || (want_res && ldr < nout))
     return fail(SYS1HIP_EINVAL, "%s: leading dimension too small (ldx=%lld ldw=%lld ldy=%lld ldr=%lld)", who,
                 (long long)ldx, (long long)ldw, (long long)ldy, (long long)ldr);
-  if (K % 8 || ldx % 8 || ldw % 8) return fail(SYS1HIP_EALIGN, "%s: K, ldx and ldw must be multiples of 8", who);
+  if (K % 8 || ldx % 8 || (!blocked && ldw % 8))
+    return fail(SYS1HIP_EALIGN, "%s: K, ldx and ldw must be multiples of 8", who);
   if (!aligned16(x) || !aligned16(w)) return fail(SYS1HIP_EALIGN, "%s: x and w must be 16-byte aligned", who);
   if (M > (1ll << 30) || N > (1ll << 30) || K > (1ll << 30))
     return fail(SYS1HIP_ERANGE, "%s: dimension above 2^30", who);
+  if (blocked && blocked_bytes(N, K) > 0x7ffffff0ll)
+    return fail(SYS1HIP_ERANGE, "%s: blocked weight above 2 GiB", who);
   return SYS1HIP_OK;
+}
+
+// The row length the plan's 2 GiB offset check sees: the caller's ldw, or
+// for a blocked weight the padded row of its layout (same total bytes).
+int64_t plan_ldw(int64_t ldw, int64_t K, int32_t epilogue) {
+  return (epilogue & SYS1HIP_EPI_BLOCKED_W) ? cdiv(K, kBlkK) * kBlkK : ldw;
 }
 
 // Launch a checked projection on `plan` with the given stream-K workspace
@@ -474,7 +502,7 @@ int check_linear(const char* who, const uint16_t* x, int64_t ldx, const uint16_t
 int launch_linear(const char* who, const Context* c, const Plan& p, hipStream_t stream, float* ws,
                   unsigned* counters, const uint16_t* x, int64_t ldx, const uint16_t* w, int64_t ldw,
                   const uint16_t* bias, const uint16_t* residual, int64_t ldr, uint16_t* y, int64_t ldy,
-                  int64_t M, int64_t N, int64_t K, int epi) {
+                  int64_t M, int64_t N, int64_t K, int epi, bool blocked) {
   (void)c;
   if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "%s: the forced kernel does not fit this call", who);
   const KernelEntry& e = kKernels[p.kernel];
@@ -493,6 +521,7 @@ int launch_linear(const char* who, const Context* c, const Plan& p, hipStream_t 
   a.M = (int)M, a.N = (int)N, a.K = (int)K, a.Nout = (int)(epi_gated(epi) ? N / 2 : N);
   a.dp_tiles = (int)std::min<int64_t>(p.dp, 1 << 30);
   a.group_m = raster_group(K);
+  a.w_kt = blocked ? (int)cdiv(K, kBlkK) : 0;
   if (grid <= 0 || grid > 0x7fffffff) return fail(SYS1HIP_ERANGE, "%s: grid of %lld workgroups", who, (long long)grid);
   hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)grid), dim3(e.threads), 0, stream, a);
   HIP_TRY(hipGetLastError());
@@ -661,8 +690,9 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
   rc = use_device(c);
   if (rc) return rc;
   const int epi = epi_id_from_flags(epilogue);
-  return launch_linear("sys1hip_linear_bf16", c, resolve(c, M, N, K, ldw, epi), c->stream, c->ws, c->counters, x,
-                       ldx, w, ldw, bias, residual, ldr, y, ldy, M, N, K, epi);
+  return launch_linear("sys1hip_linear_bf16", c, resolve(c, M, N, K, plan_ldw(ldw, K, epilogue), epi), c->stream,
+                       c->ws, c->counters, x, ldx, w, ldw, bias, residual, ldr, y, ldy, M, N, K, epi,
+                       epilogue & SYS1HIP_EPI_BLOCKED_W);
 }
 
 }  // extern "C"
@@ -748,10 +778,10 @@ int sys1hip_linear_bf16_noalloc(void* stream, const uint16_t* x, int64_t ldx, co
   // The plan is priced on every call (no cache: a cache insert would
   // allocate host memory).
   const int epi = epi_id_from_flags(epilogue);
-  const Plan p = price_plans(&d.plan_ctx, M, N, K, ldw, epi, false, false);
+  const Plan p = price_plans(&d.plan_ctx, M, N, K, plan_ldw(ldw, K, epilogue), epi, false, false);
   return launch_linear(who, &d.plan_ctx, p, s, reinterpret_cast<float*>(d.ptr),
                        reinterpret_cast<unsigned*>(d.ptr + kWorkspaceBytes), x, ldx, w, ldw, bias, residual, ldr,
-                       y, ldy, M, N, K, epi);
+                       y, ldy, M, N, K, epi, epilogue & SYS1HIP_EPI_BLOCKED_W);
 }
 
 int sys1hip_linear_rope_qkv_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_t* w,
@@ -868,10 +898,12 @@ int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const ui
   if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: null context");
   Context* c = static_cast<Context*>(ctx);
   int epi = -1;
-  if (norm == SYS1HIP_NORM_LAYER && epilogue == SYS1HIP_EPI_NONE) epi = kEpiNormLn;
-  if (norm == SYS1HIP_NORM_LAYER && epilogue == SYS1HIP_EPI_GEGLU) epi = kEpiNormLnGeglu;
-  if (norm == SYS1HIP_NORM_RMS && epilogue == SYS1HIP_EPI_NONE) epi = kEpiNormRms;
-  if (norm == SYS1HIP_NORM_RMS && epilogue == SYS1HIP_EPI_SWIGLU) epi = kEpiNormRmsSwiglu;
+  const bool blocked = epilogue & SYS1HIP_EPI_BLOCKED_W;
+  const int32_t base = epilogue & ~SYS1HIP_EPI_BLOCKED_W;
+  if (norm == SYS1HIP_NORM_LAYER && base == SYS1HIP_EPI_NONE) epi = kEpiNormLn;
+  if (norm == SYS1HIP_NORM_LAYER && base == SYS1HIP_EPI_GEGLU) epi = kEpiNormLnGeglu;
+  if (norm == SYS1HIP_NORM_RMS && base == SYS1HIP_EPI_NONE) epi = kEpiNormRms;
+  if (norm == SYS1HIP_NORM_RMS && base == SYS1HIP_EPI_SWIGLU) epi = kEpiNormRmsSwiglu;
   if (epi < 0)
     return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: unsupported norm %d with epilogue flags %d",
                 norm, epilogue);
@@ -886,10 +918,12 @@ int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const ui
   if (M == 0) return SYS1HIP_OK;
   if (!x || !w_folded || !y || (norm == SYS1HIP_NORM_LAYER && !colsum))
     return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: null pointer");
-  if (ldx < K || ldw < K || ldy < nout)
+  if (ldx < K || (!blocked && ldw < K) || ldy < nout)
     return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: leading dimension too small");
-  if (K % 8 || ldx % 8 || ldw % 8)
+  if (K % 8 || ldx % 8 || (!blocked && ldw % 8))
     return fail(SYS1HIP_EALIGN, "sys1hip_norm_linear_bf16: K, ldx and ldw must be multiples of 8");
+  if (blocked && blocked_bytes(N, K) > 0x7ffffff0ll)
+    return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: blocked weight above 2 GiB");
   if (!aligned16(x) || !aligned16(w_folded) || (colsum && !aligned16(colsum)))
     return fail(SYS1HIP_EALIGN, "sys1hip_norm_linear_bf16: x, w_folded and colsum must be 16-byte aligned");
   if (M > kNormRows)
@@ -899,7 +933,7 @@ int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const ui
     return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: dimension above 2^30");
   int rc = use_device(c);
   if (rc) return rc;
-  const Plan p = resolve(c, M, N, K, ldw, epi);
+  const Plan p = resolve(c, M, N, K, plan_ldw(ldw, K, epilogue), epi);
   if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: the forced kernel does not fit this call");
   const KernelEntry& e = kKernels[p.kernel];
   if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
@@ -919,6 +953,7 @@ int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const ui
   a.group_m = raster_group(K);
   a.stats = c->stats;
   a.colsum = colsum;
+  a.w_kt = blocked ? (int)cdiv(K, kBlkK) : 0;
   hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)p.grid), dim3(e.threads), 0, c->stream, a);
   HIP_TRY(hipGetLastError());
   return SYS1HIP_OK;
@@ -1011,6 +1046,35 @@ int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx, con
   }
   hipLaunchKernelGGL(conv_silu_inplace_kernel, dim3((unsigned)cdiv(segs * vecs, 256)), dim3(256), 0, c->stream,
                      a.y, ldy, (int)M, (int)conv_ch, (int)S, halo, a.conv_w, positions);
+  HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+
+int64_t sys1hip_blocked_weight_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || N > (1ll << 30) || K > (1ll << 30)) return -1;
+  return blocked_bytes(N, K);
+}
+
+int sys1hip_pack_blocked_weight(void* ctx, const uint16_t* w, int64_t ldw, uint16_t* packed, int64_t N,
+                                int64_t K) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_pack_blocked_weight: null context");
+  if (!w || !packed) return fail(SYS1HIP_EINVAL, "sys1hip_pack_blocked_weight: null pointer");
+  if (w == packed) return fail(SYS1HIP_EINVAL, "sys1hip_pack_blocked_weight: packed aliases w");
+  if (N <= 0 || K <= 0 || ldw < K || N > (1ll << 30) || K > (1ll << 30))
+    return fail(SYS1HIP_EINVAL, "sys1hip_pack_blocked_weight: bad shape N=%lld K=%lld ldw=%lld", (long long)N,
+                (long long)K, (long long)ldw);
+  if (K % 8 || ldw % 8) return fail(SYS1HIP_EALIGN, "sys1hip_pack_blocked_weight: K and ldw must be multiples of 8");
+  if (!aligned16(w) || !aligned16(packed))
+    return fail(SYS1HIP_EALIGN, "sys1hip_pack_blocked_weight: pointers must be 16-byte aligned");
+  if (blocked_bytes(N, K) > 0x7ffffff0ll)
+    return fail(SYS1HIP_ERANGE, "sys1hip_pack_blocked_weight: blocked weight above 2 GiB");
+  Context* c = static_cast<Context*>(ctx);
+  int rc = use_device(c);
+  if (rc) return rc;
+  const int64_t total = blocked_bytes(N, K) / 16;
+  hipLaunchKernelGGL(pack_blocked_kernel, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, c->stream,
+                     reinterpret_cast<const __bf16*>(w), ldw, reinterpret_cast<i32x4*>(packed), N, K, cdiv(K, kBlkK),
+                     total);
   HIP_TRY(hipGetLastError());
   return SYS1HIP_OK;
 }

@@ -51,15 +51,18 @@ def _rows(t: torch.Tensor, name: str) -> tuple[torch.Tensor, int]:
 
 def linear_bf16(dev: HipDevice, x: torch.Tensor, w: torch.Tensor, out: torch.Tensor,
                 epilogue: int = _lib.EPI_NONE, bias: torch.Tensor | None = None,
-                residual: torch.Tensor | None = None) -> torch.Tensor:
-    """Raw call of sys1hip_linear_bf16 on 2-D views: out = epi(x . w^T)."""
+                residual: torch.Tensor | None = None, n: int | None = None) -> torch.Tensor:
+    """Raw call of sys1hip_linear_bf16 on 2-D views: out = epi(x . w^T).
+    With EPI_BLOCKED_W in `epilogue`, w is a blocked weight (BlockedWeight
+    storage) of `n` rows."""
     M, K = x.shape
-    N = w.shape[0]
+    blocked = bool(epilogue & _lib.EPI_BLOCKED_W)
+    N = n if blocked else w.shape[0]
     dev.follow_torch_stream()
     _lib.check(dev._L.sys1hip_linear_bf16(
         dev.ctx,
         _vp(x.data_ptr()), x.stride(0) if M > 1 else K,
-        _vp(w.data_ptr()), w.stride(0),
+        _vp(w.data_ptr()), K if blocked else w.stride(0),
         _vp(bias.data_ptr()) if bias is not None else None,
         _vp(residual.data_ptr()) if residual is not None else None,
         (residual.stride(0) if M > 1 else residual.shape[1]) if residual is not None else 0,
@@ -68,26 +71,49 @@ def linear_bf16(dev: HipDevice, x: torch.Tensor, w: torch.Tensor, out: torch.Ten
     return out
 
 
+def pack_blocked_weight(weight: torch.Tensor, device: HipDevice | None = None) -> torch.Tensor:
+    """[N, K] row-major -> the blocked layout (sys1hip_pack_blocked_weight):
+    32-row x 64-column blocks of 4 KB, so the weight-streaming kernels read
+    4 KB of contiguous memory per 32 rows and k-step.  Returns a flat bf16
+    tensor; calls on it pass EPI_BLOCKED_W and the row count."""
+    dev = device or load_device(weight.device.index or 0)
+    _check_operand(weight, "weight", dev)
+    w = weight.contiguous()
+    N, K = w.shape
+    nbytes = dev._L.sys1hip_blocked_weight_bytes(N, K)
+    if nbytes < 0:
+        raise ValueError(f"bad weight shape {tuple(w.shape)}")
+    packed = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=w.device)
+    dev.follow_torch_stream()
+    _lib.check(dev._L.sys1hip_pack_blocked_weight(dev.ctx, _vp(w.data_ptr()), K, _vp(packed.data_ptr()),
+                                                   N, K), dev.ctx)
+    return packed
+
+
 class Linear:
-    """y = x.W^T (+ b), weight [out, in] bf16 on the device."""
+    """y = x.W^T (+ b), weight [out, in] bf16 on the device.  blocked=True
+    stores the weight in the blocked layout (pack_blocked_weight) instead of
+    candle's row-major [out, in]: same results, read as contiguous 4 KB
+    blocks by the weight-streaming kernels."""
 
     def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None = None,
-                 device: HipDevice | None = None):
+                 device: HipDevice | None = None, blocked: bool = False):
         self.device = device or load_device(weight.device.index or 0)
         if weight.dim() != 2:
             raise ValueError(f"weight must be [out, in], got shape {tuple(weight.shape)}")
         _check_operand(weight, "weight", self.device)
-        self.weight = weight.contiguous()
+        self.blocked = blocked
+        self.weight = pack_blocked_weight(weight, self.device) if blocked else weight.contiguous()
         if bias is not None:
             _check_operand(bias, "bias", self.device)
             if bias.shape != (weight.shape[0],):
                 raise ValueError(f"bias must be [{weight.shape[0]}], got {tuple(bias.shape)}")
             bias = bias.contiguous()
         self.bias = bias
-        self.out_features, self.in_features = self.weight.shape
+        self.out_features, self.in_features = weight.shape
 
     def _epilogue(self, residual, gelu: bool) -> int:
-        e = _lib.EPI_NONE
+        e = _lib.EPI_BLOCKED_W if self.blocked else _lib.EPI_NONE
         if self.bias is not None:
             e |= _lib.EPI_BIAS
         if gelu:
@@ -115,7 +141,7 @@ class Linear:
             if r2.shape != o2.shape:
                 raise ValueError(f"residual must match the output shape {tuple(o2.shape)}")
         linear_bf16(self.device, x2, self.weight, o2, self._epilogue(residual, gelu),
-                    self.bias, r2)
+                    self.bias, r2, n=self.out_features)
         return out
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None,
@@ -149,7 +175,7 @@ class GatedLinear:
 
     def __init__(self, weight: torch.Tensor | None = None, activation: str = "gelu",
                  gate: torch.Tensor | None = None, up: torch.Tensor | None = None,
-                 device: HipDevice | None = None, packed: bool = False):
+                 device: HipDevice | None = None, packed: bool = False, blocked: bool = False):
         if weight is None:
             if gate is None or up is None:
                 raise ValueError("pass either weight [2I, K] or both gate and up")
@@ -162,6 +188,10 @@ class GatedLinear:
                              f"got {tuple(weight.shape)}")
         self.epilogue = _lib.EPI_GEGLU if activation == "gelu" else _lib.EPI_SWIGLU
         self.weight = weight.contiguous() if packed else pack_gated_weight(weight, self.device)
+        if blocked:  # the gate/up interleave first, then the blocked layout of that
+            self.weight = pack_blocked_weight(self.weight, self.device)
+            self.epilogue |= _lib.EPI_BLOCKED_W
+        self.rows = weight.shape[0]
         self.in_features = weight.shape[1]
         self.out_features = weight.shape[0] // 2
 
@@ -173,7 +203,7 @@ class GatedLinear:
         o2, _ = _rows(out, "out")
         if o2.shape != (x2.shape[0], self.out_features):
             raise ValueError(f"out must be [{x2.shape[0]}, {self.out_features}]")
-        return linear_bf16(self.device, x2, self.weight, o2, self.epilogue)
+        return linear_bf16(self.device, x2, self.weight, o2, self.epilogue, n=self.rows)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         out = torch.empty(*x.shape[:-1], self.out_features, dtype=torch.bfloat16, device=x.device)

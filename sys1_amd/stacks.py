@@ -155,22 +155,29 @@ class ProjectionStack:
 
     conv=True fuses the DeltaNet causal conv + SiLU into each in_proj
     (Proj.conv_ch columns; conv weights N(0, 0.5^2) or `conv_weights`
-    [layer] -> [conv_ch, 4]); the calls then need per-token positions."""
+    [layer] -> [conv_ch, 4]); the calls then need per-token positions.
+
+    blocked=True stores the weights in the blocked layout
+    (linear.pack_blocked_weight: contiguous 4 KB per 32 rows and k-step,
+    what the weight-streaming kernels read best), after any gate/up packing
+    and norm folding; the in_proj calls with the conv fused keep the
+    row-major layout."""
 
     def __init__(self, cfg: StackConfig, dev: HipDevice, max_tokens: int, seed: int = 0,
                  weights: list[list[torch.Tensor]] | None = None, w_std: float = 0.02,
                  norms: bool = False, norm_weights: list[list[torch.Tensor | None]] | None = None,
                  norm_eps: dict[str, float] | None = None, conv: bool = False,
-                 conv_weights: list[torch.Tensor | None] | None = None):
+                 conv_weights: list[torch.Tensor | None] | None = None, blocked: bool = False):
         self.cfg = cfg
         self.dev = dev
         self.max_tokens = max_tokens
         d = dev.torch_device
         g = torch.Generator(device=d)
         g.manual_seed(seed)
-        from .linear import pack_gated_weight
+        from .linear import pack_blocked_weight, pack_gated_weight
         from .norm import fold_norm_weight
         self.norms = norms
+        self.blocked = blocked
         self.conv = conv
         self.conv_w: list[torch.Tensor | None] = []
         self.norm_eps = dict(NORM_EPS, **(norm_eps or {}))
@@ -192,6 +199,8 @@ class ProjectionStack:
                     if gw is None:
                         gw = torch.ones(p.K) if p.norm == "layer" else torch.zeros(p.K)
                     w, c = fold_norm_weight(w, gw, p.norm, dev)
+                if blocked and not (conv and p.conv_ch):
+                    w = pack_blocked_weight(w, dev)
                 ws.append(w)
                 cs.append(c)
             self.weights.append(ws)
@@ -254,12 +263,15 @@ class ProjectionStack:
                 elif self.norms and p.norm:
                     c = self.colsums[li][pi]
                     calls.append((p, self._norm_fn, (
-                        src, ldx, w.data_ptr(), w.stride(0), c.data_ptr() if c is not None else None,
+                        src, ldx, w.data_ptr(), p.K if self.blocked else w.stride(0),
+                        c.data_ptr() if c is not None else None,
                         _lib.NORM_LAYER if p.norm == "layer" else _lib.NORM_RMS, self.norm_eps[p.norm],
-                        dst.data_ptr(), dst.stride(0), M, p.N, p.K, p.epi)))
+                        dst.data_ptr(), dst.stride(0), M, p.N, p.K,
+                        p.epi | (_lib.EPI_BLOCKED_W if self.blocked else 0))))
                 else:
-                    calls.append((p, self._fn, (src, ldx, w.data_ptr(), w.stride(0), None, rptr, ldr,
-                                                dst.data_ptr(), dst.stride(0), M, p.N, p.K, p.epi)))
+                    calls.append((p, self._fn, (src, ldx, w.data_ptr(), p.K if self.blocked else w.stride(0),
+                                                None, rptr, ldr, dst.data_ptr(), dst.stride(0), M, p.N, p.K,
+                                                p.epi | (_lib.EPI_BLOCKED_W if self.blocked else 0))))
         return calls
 
     def prepare(self, x: torch.Tensor, M: int, positions: torch.Tensor | None = None):

@@ -87,7 +87,7 @@ def _call(x=_P, ldx=64, w=_P, ldw=64, bias=None, res=None, ldr=0, y=_P, ldy=64, 
 
 @pytest.mark.parametrize("kwargs,code", [
     (dict(ctx=None), _lib.EINVAL),
-    (dict(epi=32), _lib.EINVAL),                      # unknown flag
+    (dict(epi=64), _lib.EINVAL),                      # unknown flag
     (dict(epi=_lib.EPI_GELU), _lib.EINVAL),           # gelu needs bias
     (dict(epi=_lib.EPI_GEGLU | _lib.EPI_SWIGLU), _lib.EINVAL),
     (dict(N=0), _lib.EINVAL),

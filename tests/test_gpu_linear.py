@@ -513,3 +513,34 @@ def test_stream_switch_waits_for_the_old_stream(dev, orc):
     finally:
         torch.cuda.synchronize()
         dev.follow_torch_stream()
+
+
+def test_blocked_weight_layout_is_bitwise_row_major(dev, orc):
+    """A weight in the blocked layout (pack_blocked_weight: 32-row x 64-k
+    blocks, rows and K zero-padded) gives the row-major weight's results bit
+    for bit on every kernel (the same values reach the same LDS and register
+    positions): plain, residual and gated epilogues, N and K not multiples
+    of the block, tile, stream-K and skinny plans."""
+    from sys1_amd import kernel_names
+    from sys1_amd.linear import GatedLinear, Linear
+    names = kernel_names()
+    try:
+        for kid, name in enumerate(names):
+            Ms = [70] if name.startswith(("stream_", "skinny_")) else [300]
+            for M in Ms:
+                for (N, K) in [(200, 328), (96, 1000)]:
+                    print(f"[gpu] blocked {name} M={M} N={N} K={K}", flush=True)
+                    x, w = _inputs(orc, M, N, K, 61 + N)
+                    xg, wg = to_gpu_bf16(x, torch), to_gpu_bf16(w, torch)
+                    res = to_gpu_bf16(orc.fill_normal((M, N), 62), torch)
+                    dev.set_kernel(kid)
+                    rm, bl = Linear(wg, device=dev), Linear(wg, device=dev, blocked=True)
+                    assert torch.equal(rm(xg), bl(xg)), f"{name} none"
+                    assert torch.equal(rm(xg, residual=res), bl(xg, residual=res)), f"{name} residual"
+                    gated = not name.startswith("skinny_") or int(name.split("_")[1].split("x")[1]) % 32 == 0
+                    if gated and N % 32 == 0:
+                        g_rm = GatedLinear(wg, "silu", device=dev)
+                        g_bl = GatedLinear(wg, "silu", device=dev, blocked=True)
+                        assert torch.equal(g_rm(xg), g_bl(xg)), f"{name} swiglu"
+    finally:
+        dev.set_kernel(-1)
