@@ -75,6 +75,13 @@ def parse():
     ap.add_argument("--calibration-copy", type=int, default=0, metavar="MIB",
                     help="after the run, 8 bf16 negations of MIB MiB (read MIB, write MIB): the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--vs-torch", action="store_true",
+                    help="with --workload and --tokens: time each distinct projection shape of the stack (no "
+                         "epilogue) on this library and on torch's matmul (hipBLASLt) over rotated weight "
+                         "copies larger than the MALL, print a table and exit")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="reduce a rocprofv3 kernel_trace.csv of a bench run (with --workload, --tokens) "
+                         "to per-projection kernel durations and their HBM / MFMA rates, and exit")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
                     help="reduce rocprofv3 counter_collection.csv files to per-kernel averages "
                          "per dispatch and exit (no GPU use)")
@@ -100,6 +107,89 @@ def pmc_summary(paths: list[str]) -> None:
         n = max(len(v) for v in cs.values())
         vals = ", ".join(f"{c}={sum(v) / len(v):.6g}" for c, v in sorted(cs.items()))
         print(f"{n:6d} dispatches | {vals} | {name[:160]}")
+
+
+def trace_summary(path: str, workload: str, tokens: int | None) -> None:
+    """Per-projection kernel durations from a rocprofv3 kernel trace of a
+    bench run: the projection kernels (sys1 GEMM kernels, in dispatch order)
+    map onto the stack's projection sequence, layer after layer; the last
+    whole steps are averaged.  With --tokens, each projection's algorithmic
+    bytes and FLOP give its HBM and MFMA rates."""
+    import csv
+    import collections
+    from sys1_amd.stacks import CONFIGS
+    cfg = CONFIGS[WORKLOADS[workload][0]]()
+    seq = [p for layer in cfg.layers for p in layer]
+    rows = [r for r in csv.DictReader(open(path))
+            if "gemm_tile_kernel" in r["Kernel_Name"] or "skinny_kernel" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    steps = len(rows) // len(seq)
+    rows = rows[len(rows) - steps * len(seq):]
+    per = collections.defaultdict(list)
+    names = {}
+    for i, r in enumerate(rows):
+        p = seq[i % len(seq)]
+        per[p.name].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        names.setdefault(p.name, r["Kernel_Name"].split("(")[0].replace("void sys1::", ""))
+    total = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows) / steps / 1e3
+    span = (int(rows[-1]["End_Timestamp"]) - int(rows[0]["Start_Timestamp"])) / steps / 1e3
+    print(f"{workload} M={tokens}: {steps} steps; kernel time per step {total:.1f} us, "
+          f"first start to last end per step {span:.1f} us")
+    first = {p.name: p for p in seq}
+    for name, d in per.items():
+        us = sum(d) / len(d) / 1e3
+        line = f"  {name:16s} {names[name]:48s} {len(d):5d} launches  {us:8.2f} us"
+        if tokens:
+            p = first[name]
+            line += (f"  {p.bytes(tokens) / us / 1e3:8.1f} GB/s ({p.bytes(tokens) / us / 1e3 / PEAK_HBM_GBS:.3f})"
+                     f"  {p.flops(tokens) / us / 1e6:7.1f} TFLOP/s")
+        print(line)
+
+
+def vs_torch(workload: str, tokens: int, reps: int = 30) -> None:
+    """Each distinct (N, K) projection shape of the stack at M = tokens, as
+    a plain GEMM: this library (its automatic plan, blocked weights) and
+    torch.matmul(x, w.T) (hipBLASLt), each over enough rotated weight copies
+    to exceed the 256 MB MALL, so every call streams its weight from HBM as
+    in a deep stack.  Times are HIP events over back-to-back calls (launch
+    gaps included); a rocprofv3 kernel trace of the same run gives the
+    kernel durations."""
+    import torch
+    from sys1_amd.device import HipDevice
+    from sys1_amd.linear import Linear
+    from sys1_amd.stacks import CONFIGS
+    cfg = CONFIGS[WORKLOADS[workload][0]]()
+    dev = HipDevice(0)
+    shapes = []
+    for p in cfg.layers[0]:
+        if (p.N, p.K) not in shapes:
+            shapes.append((p.N, p.K))
+    x = torch.randn(tokens, max(k for _, k in shapes), device="cuda:0").to(torch.bfloat16)
+    print(f"{workload} M={tokens}: plain GEMMs over rotated weights (HIP events, launch gaps included)")
+    for N, K in shapes:
+        copies = max(2, (300 << 20) // (2 * N * K) + 1)
+        ws = [(torch.randn(N, K, device="cuda:0") * 0.02).to(torch.bfloat16) for _ in range(copies)]
+        ours = [Linear(w, device=dev, blocked=True) for w in ws]
+        xk = x[:, :K].contiguous()
+        y = torch.empty(tokens, N, dtype=torch.bfloat16, device="cuda:0")
+        res = {}
+        for tag, fn in (("sys1hip", lambda i: ours[i % copies].forward_into(xk, y)),
+                        ("torch", lambda i: torch.matmul(xk, ws[i % copies].t(), out=y))):
+            for i in range(copies):
+                fn(i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(reps * copies // max(1, copies // 4) if copies < 8 else reps):
+                fn(i)
+            e1.record()
+            torch.cuda.synchronize()
+            n = reps * copies // max(1, copies // 4) if copies < 8 else reps
+            res[tag] = e0.elapsed_time(e1) * 1e3 / n
+        kname = dev.query_kernel(tokens, N, K, 0)[1]
+        print(f"  N={N:6d} K={K:6d}  sys1hip {res['sys1hip']:8.2f} us ({kname})  torch {res['torch']:8.2f} us")
+        del ws, ours
+        torch.cuda.empty_cache()
 
 
 def load_traffic(workload: str, kernel: str) -> dict | None:
@@ -232,6 +322,14 @@ def main():
     args = parse()
     if args.pmc_summary:
         pmc_summary(args.pmc_summary)
+        return
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.workload, args.tokens)
+        return
+    if args.vs_torch:
+        if not args.tokens:
+            raise SystemExit("--vs-torch needs --tokens")
+        vs_torch(args.workload, args.tokens)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported in this build "
