@@ -141,14 +141,6 @@ ORC_EXPORT void orc_swiglu(const float* gate, int64_t ldg, const float* up, int6
             out[m * ldout + j] = orc_silu(gate[m * ldg + j]) * up[m * ldu + j];
 }
 
-/* Residual add y += r  (src/archs/modernbert.rs:883,886; src/archs/qwen35_text.rs:938-939). */
-ORC_EXPORT void orc_add_inplace(float* y, int64_t ldy, const float* r, int64_t ldr,
-                                int64_t M, int64_t N) {
-    #pragma omp parallel for schedule(static)
-    for (int64_t m = 0; m < M; ++m)
-        for (int64_t n = 0; n < N; ++n) y[m * ldy + n] += r[m * ldr + n];
-}
-
 /* LayerNorm with weight and bias over the last dim, eps given
  * (candle_nn::layer_norm; Laya scorer norm, src/models/laya.rs:258).
  * Mean and variance accumulated in double. */

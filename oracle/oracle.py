@@ -44,7 +44,6 @@ def lib():
         L.orc_silu.restype = ctypes.c_float
         L.orc_geglu.argtypes = [_f32p, _i64, _f32p, _i64, _i64, _i64]
         L.orc_swiglu.argtypes = [_f32p, _i64, _f32p, _i64, _f32p, _i64, _i64, _i64]
-        L.orc_add_inplace.argtypes = [_f32p, _i64, _f32p, _i64, _i64, _i64]
         L.orc_layer_norm.argtypes = [_f32p, _i64, _f32p, _f32p, ctypes.c_float, _f32p, _i64, _i64, _i64]
         L.orc_rms_norm.argtypes = [_f32p, _i64, _f32p, ctypes.c_float, _f32p, _i64, _i64, _i64]
         L.orc_conv_silu.argtypes = [_f32p, _i64, _f32p, ctypes.POINTER(ctypes.c_int32), _i64, _i64, _i64,
