@@ -295,17 +295,20 @@ constexpr int64_t kCachedWeightBytes = 32 << 20;
 constexpr int64_t kRereadWeightBytes = 128 << 20;  // half the 256 MB MALL
 
 // The skinny-M kernel for a call, or -1.  A skinny workgroup reads its BN
-// weight rows and its BM rows of x over the whole K, so the busiest CU
-// moves
-//   ceil(tiles / CUs) * (BM + BN) * K * 2 bytes
-// through its load path; the shape with the fewest such bytes is taken
-// (ties: the first listed), and the skinny kernels win while that stays
-// within kSkinnyCuBytes (measured over the ModernBERT-base/large and
-// Qwen3.5-small projections at M = 16..256: up to ~420 KB per CU ran
-// 1.1-1.7x faster than the stream-K and tile kernels, ~600 KB tied, more
-// lost).  Above kSkinnyWeightBytes the weight is streamed from HBM and
-// needs the stream-K schedule's spread of K over every CU.
-constexpr int64_t kSkinnyMaxM = 512;
+// weight rows and its BM rows of x over the whole K, and one round of
+// tiles (at most one workgroup per CU) is allowed, so each CU moves
+//   (BM + BN) * K * 2 bytes
+// through its load path; the one-round shape with the fewest such bytes is
+// taken (ties: the first listed), and the skinny kernels win while that
+// stays within kSkinnyCuBytes.  Measured over the ModernBERT-base/large and
+// Qwen3.5-small projections at M = 16..4096: one round at up to ~420 KB per
+// CU ran 1.1-1.9x faster than the stream-K and tile kernels, ~600 KB tied,
+// more lost; shapes needing two or more rounds lost (the Qwen3.5-small
+// q/k/v at M = 64 on 288 16-wide tiles: 26 against 23 us; ModernBERT-base
+// Wqkv at M = 1024 on three rounds of 64x48 tiles: 24 against 15 us).
+// Above kSkinnyWeightBytes the weight is streamed from HBM and needs the
+// stream-K schedule's spread of K over every CU.
+constexpr int64_t kSkinnyMaxM = 4096;
 constexpr int64_t kSkinnyWeightBytes = 32 << 20;
 constexpr int64_t kSkinnyCuBytes = 512 << 10;
 
@@ -316,8 +319,8 @@ int skinny_pick(const Context* c, int64_t M, int64_t N, int64_t K, int64_t ldw, 
   for (int id = 0; id < kNumKernels; ++id) {
     const KernelEntry& e = kKernels[id];
     if (!e.skinny || !e.fn[epi]) continue;
-    const int64_t tiles = cdiv(M, e.bm) * cdiv(N, e.bn);
-    const int64_t bytes = cdiv(tiles, c->cus) * (e.bm + e.bn) * K * 2;
+    if (cdiv(M, e.bm) * cdiv(N, e.bn) > c->cus) continue;  // one round
+    const int64_t bytes = (e.bm + e.bn) * K * 2;
     if (best < 0 || bytes < best_bytes) best = id, best_bytes = bytes;
   }
   return best >= 0 && best_bytes <= kSkinnyCuBytes ? best : -1;
