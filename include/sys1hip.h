@@ -123,8 +123,11 @@ SYS1HIP_API int sys1hip_pack_gated_weight(void* ctx, const uint16_t* w, uint16_t
                               int64_t N, int64_t K);
 
 /* Kernel choice for a shape (for profiling and reports): returns the kernel
- * id the dispatcher would launch, and writes its name into `name` (up to
- * `cap` bytes including the terminator). */
+ * id sys1hip_linear_bf16 would launch for these epilogue flags, and writes
+ * its name into `name` (up to `cap` bytes including the terminator).  It
+ * covers sys1hip_linear_bf16 only: the RoPE, pre-norm and conv entry points
+ * restrict or extend the choice (head-aligned tiles, norm epilogues), so
+ * their kernel can differ. */
 SYS1HIP_API int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epilogue,
                          char* name, int64_t cap);
 
