@@ -66,3 +66,40 @@ def test_noalloc_matches_the_context_entry_point(orc):
     rc = L.sys1hip_linear_bf16_noalloc(stream, _ptr(x), 64, _ptr(w), 64, None, None, 0, _ptr(y), 64,
                                        8, 64, 60, 0)
     assert rc == _lib.EALIGN
+
+
+def test_noalloc_under_graph_capture(orc):
+    """The entry point inside a captured HIP graph: each replay, with eager
+    calls of the same entry point (which overwrite the static workspace) and
+    synchronisations between replays, equals the eager result bit for bit.
+    Covers a stream-K plan (workspace and counters) and a skinny plan."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from sys1_amd import _lib
+    L = _lib.load()
+    for (M, N, K, epi) in [(64, 8192, 4096, _lib.EPI_RESIDUAL), (48, 3072, 1024, 0)]:
+        print(f"[gpu] noalloc graph M={M} N={N} K={K} epi={epi}", flush=True)
+        x = to_gpu_bf16(orc.fill_normal((M, K), 7 + M), torch)
+        w = to_gpu_bf16(orc.fill_normal((N, K), 8 + N, 0.02), torch)
+        res = to_gpu_bf16(orc.fill_normal((M, N), 9), torch) if epi == _lib.EPI_RESIDUAL else None
+        x2 = to_gpu_bf16(orc.fill_normal((M, K), 11), torch)
+        y_eager = torch.empty(M, N, dtype=torch.bfloat16, device="cuda:0")
+        y_graph = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda:0")
+        y_other = torch.empty(M, N, dtype=torch.bfloat16, device="cuda:0")
+        s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(_call(L, L.sys1hip_linear_bf16_noalloc, s, x, w, y_eager, res=res, epi=epi))
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            cs = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            _lib.check(_call(L, L.sys1hip_linear_bf16_noalloc, cs, x, w, y_graph, res=res, epi=epi))
+        torch.cuda.synchronize()
+        for r in range(4):
+            y_graph.fill_(float("nan"))
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y_graph, y_eager), f"replay {r}: M={M} N={N} K={K} epi={epi}"
+            # eager work between replays, on the same static workspace
+            _lib.check(_call(L, L.sys1hip_linear_bf16_noalloc, s, x2, w, y_other, res=res, epi=epi))
+            torch.cuda.synchronize()
+        del g
