@@ -184,6 +184,13 @@ __device__ __forceinline__ rsrc_t make_rsrc_uniform(const void* base, int bytes)
 __device__ __forceinline__ void dma16(rsrc_t r, unsigned off, lds_void* lds_base) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_base, 16, (int)off, 0, 0, 0);
 }
+// Cache-policy bits of a gfx950 buffer access: nt (non-temporal: streamed
+// through the caches rather than kept).
+constexpr int kCachePolicyNt = 2;
+template <int POL>
+__device__ __forceinline__ void dma16_pol(rsrc_t r, unsigned off, lds_void* lds_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds_base, 16, (int)off, 0, 0, POL);
+}
 
 // s_waitcnt vmcnt(N) with the LDS and export counters left unconstrained.
 template <int N>

@@ -226,7 +226,10 @@ struct TileWalk {
 // PW: producer waves.  0: every wave issues its share of the refills between
 // its MFMAs.  PW > 0: PW extra waves issue all of them and do nothing else,
 // so a refill instruction that stalls issue while the load path drains
-// stalls no matrix work (tile schedule only).
+// stalls no matrix work.  Under stream-K the compute waves then also wait
+// for their partial stores (before the arrival counter) without draining
+// the refills in flight: a wave's vmcnt covers every vector memory access
+// it issued, and with producer waves those are its stores alone.
 template <int BM, int BN, int WM, int WN, int STAGES, int BK_, int OCC, bool STREAMK, int EPI, int PW = 0>
 __global__ __launch_bounds__((WM * WN + PW) * 64)
 __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_tile_kernel(GemmArgs a) {
@@ -248,7 +251,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
 
   constexpr bool kConv = epi_base(EPI) == kEpiConvSilu;
   static_assert(!kConv || WM == 1, "conv epilogue: one wave row per tile");
-  static_assert(PW == 0 || (!STREAMK && !kConv), "producer waves: plain tile schedule");
+  static_assert(PW == 0 || !kConv, "producer waves: no conv epilogue");
   const TileWalk walk(a.M, a.N, a.K, BM, BN, BK, STREAMK ? a.dp_tiles : 1 << 30, a.group_m,
                       kConv ? kConvHalo : 0);
   if (walk.steps() == 0) return;
@@ -326,7 +329,11 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
   auto dma_one = [&](const Refill& r, int i) {
     unsigned off = src_off[i];
     if (r.kleft < BK && (lpos ^ lds_swz<BK>(dma_row(i))) * 8 >= r.kleft) off = kOutOfRange;
-    dma16(i < kXDma ? r.xr : r.wr, off, (lds_void*)(r.base + (i * kDW + dwave) * 1024));
+    // Stream-K reads each weight byte once per call: its weight loads are
+    // non-temporal (nt), measured 4-8% faster on the weight streams than
+    // the default policy.
+    if (i < kXDma || !STREAMK) dma16(i < kXDma ? r.xr : r.wr, off, (lds_void*)(r.base + (i * kDW + dwave) * 1024));
+    else dma16_pol<kCachePolicyNt>(r.wr, off, (lds_void*)(r.base + (i * kDW + dwave) * 1024));
   };
   auto issue_advance = [&]() {
     if (++is_kt == isg.kt1) {

@@ -132,7 +132,8 @@ def test_every_conv_kernel_and_grid(dev, orc):
     from sys1_amd import kernel_names
     M, N, C, K = 700, 544, 384, 328
     x, w, cw, g, pos = _case(orc, M, N, C, K, 7, False)
-    names = [n for n in kernel_names() if "_w1x" in n]
+    # (waves spanning every row; producer-wave shapes have no conv epilogue)
+    names = [n for n in kernel_names() if "_w1x" in n and "_p" not in n.split("_w1x")[1]]
     assert len(names) >= 3
     try:
         for name in names:

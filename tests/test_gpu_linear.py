@@ -213,7 +213,7 @@ def test_stream_k_is_deterministic_and_rearms(dev, orc):
         dev.set_kernel(-1)
 
 
-@pytest.mark.parametrize("kname", ["stream_128x128_s4_w2x2", "stream_128x256_s3_w2x4"])
+@pytest.mark.parametrize("kname", ["stream_128x128_s4_w2x2_p4", "stream_128x256_s3_w2x4"])
 def test_hybrid_tile_then_stream_phase(dev, orc, kname):
     """Stream-K kernels on large M: the first dp tiles run whole, the rest
     are split over every workgroup.  Every split (pure stream-K, one tile
