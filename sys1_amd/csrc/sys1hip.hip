@@ -250,6 +250,26 @@ int64_t max_grid(const Context* c, int id, int epi, int64_t M, int64_t N, int64_
   return g;
 }
 
+// Between two stream-K plans the model prices the same (both at the weight
+// stream's HBM floor), whether plan (id, dp) is to be preferred to `best`:
+// the shorter tile height that still covers M (fewer padded rows, less x
+// and partial traffic), then producer waves, then more tiles run whole
+// before the stream phase (fewer split tiles).  Measured on the Qwen3.5-27B
+// weights: at M = 16 the 32-row shape ran down / q_k_v / in_proj 5-12%
+// faster than the 64-row one; at M = 128 the gate/up projection ran
+// 86.7 us on 128x128 producer-wave tiles with one whole round of tiles
+// first, against 88.7 us on 128x256 tiles and 90.0 us in pure stream-K.
+bool stream_preferred(int id, int64_t dp, const Plan& best, int64_t M) {
+  const KernelEntry& a = kKernels[id];
+  const KernelEntry& b = kKernels[best.kernel];
+  if (!a.streamk || !b.streamk) return false;
+  const bool afit = a.bm >= M, bfit = b.bm >= M;
+  if (afit != bfit) return afit;
+  if (a.bm != b.bm) return afit ? a.bm < b.bm : a.bm > b.bm;
+  if ((a.pw > 0) != (b.pw > 0)) return a.pw > 0;
+  return id == best.kernel && dp > best.dp;
+}
+
 // Prices kernel `id` on `grid` workgroups and keeps it in *best when it is
 // cheaper.  Tile kernels run every tile whole.  Stream-K kernels try: pure
 // stream-K, the hybrid whose stream phase is the last partial round of
@@ -271,7 +291,8 @@ void consider(const Context* c, int id, int epi, int64_t M, int64_t N, int64_t K
   for (int64_t dp : cand) {
     if (dp < 0 || (tiles - dp) * (e.threads / 64) > kCounterSlots) continue;
     const double cost = model_cost(c, id, epi, M, N, K, grid, dp);
-    if (cost < best->cost * 0.999) {
+    const bool tie = best->kernel >= 0 && cost <= best->cost * 1.001 && cost >= best->cost * 0.999;
+    if (cost < best->cost * 0.999 || (tie && stream_preferred(id, dp, *best, M))) {
       best->kernel = id, best->grid = grid, best->dp = dp, best->cost = cost;
     }
   }
