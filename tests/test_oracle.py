@@ -222,6 +222,37 @@ def test_conv_silu_bf16_against_torch_bf16_ops(orc):
     assert (diff == 0).mean() > 0.99
 
 
+def test_conv_tap_rounding_gap(orc):
+    """The GPU conv accumulates its four taps in f32 and rounds once; the
+    reference rounds every product and partial sum to bf16
+    (src/kernels/qwen35.cu:18-24).  On the same bf16 inputs (unit-normal
+    projection, conv weights N(0, 0.25), ragged sequences) the two differ by
+    ~4.2e-3 relative Frobenius and ~1e-2 max-abs/max, which is the whole of
+    the GPU in_proj+conv error against the reference chain; against the exact
+    f64 conv, the single rounding is the closer of the two."""
+    rng = np.random.default_rng(0)
+    M, C = 4096, 512
+    p = orc.round_bf16(rng.standard_normal((M, C)).astype(np.float32))
+    w = orc.round_bf16((rng.standard_normal((C, 4)) * 0.5).astype(np.float32))
+    pos = np.concatenate([np.arange(n) for n in (1000, 900, 1200, 996)]).astype(np.int32)
+    ref = orc.conv_silu(p, w, pos, bf16=True)
+    once = orc.round_bf16(orc.conv_silu(p, w, pos, bf16=False))
+    d = once - ref
+    rel = np.linalg.norm(d) / np.linalg.norm(ref)
+    assert 2e-3 < rel < 6e-3, rel
+    assert np.abs(d).max() <= 1.5e-2 * np.abs(ref).max()
+    exact = np.zeros((M, C))
+    for tap in range(4):
+        back = 3 - tap
+        shifted = np.zeros((M, C))
+        shifted[back:] = p[:M - back]
+        exact += np.where((pos >= back)[:, None], shifted, 0.0) * w[:, tap].astype(np.float64)[None, :]
+    exact = exact / (1 + np.exp(-exact))
+    err_ref = np.linalg.norm(ref - exact) / np.linalg.norm(exact)
+    err_once = np.linalg.norm(once - exact) / np.linalg.norm(exact)
+    assert err_once < 0.6 * err_ref, (err_once, err_ref)
+
+
 def test_conv_silu_closed_forms(orc):
     """Identity tap: weight 1 on the newest tap gives silu(p); an impulse
     at one row spreads to the next three rows of its sequence only, with the
