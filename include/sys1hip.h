@@ -131,6 +131,16 @@ SYS1HIP_API int sys1hip_pack_gated_weight(void* ctx, const uint16_t* w, uint16_t
 SYS1HIP_API int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epilogue,
                          char* name, int64_t cap);
 
+/* The same choice without a device or context, for planning and host-side
+ * tests (no counterpart in the reference): the plan sys1hip_linear_bf16
+ * would make on a GPU with `cus` compute units, priced with the shapes'
+ * fitted occupancies (a device context uses the runtime's, which agree
+ * unless an epilogue variant spills).  Returns the kernel id, writes the
+ * workgroup count to *grid (nullable) and the plan's name as
+ * sys1hip_query_kernel does. */
+SYS1HIP_API int sys1hip_plan_kernel(int32_t cus, int64_t M, int64_t N, int64_t K, int32_t epilogue,
+                        int64_t* grid, char* name, int64_t cap);
+
 /* Force a kernel id for subsequent calls on this context (-1 = automatic
  * choice).  Used by the tile sweep and by tests that cover every kernel. */
 SYS1HIP_API int sys1hip_set_kernel(void* ctx, int32_t kernel_id);

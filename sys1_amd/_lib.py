@@ -39,7 +39,7 @@ EXPORTS = (
     "sys1hip_kernel_count", "sys1hip_kernel_name", "sys1hip_set_grid",
     "sys1hip_set_dp_tiles", "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
     "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_linear_bf16_noalloc",
-    "sys1hip_blocked_weight_bytes", "sys1hip_pack_blocked_weight",
+    "sys1hip_blocked_weight_bytes", "sys1hip_pack_blocked_weight", "sys1hip_plan_kernel",
 )
 
 
@@ -80,6 +80,7 @@ def load() -> ctypes.CDLL:
     L.sys1hip_blocked_weight_bytes.restype = i64
     L.sys1hip_pack_blocked_weight.argtypes = [vp, vp, i64, vp, i64, i64]
     L.sys1hip_query_kernel.argtypes = [vp, i64, i64, i64, i32, ctypes.c_char_p, i64]
+    L.sys1hip_plan_kernel.argtypes = [i32, i64, i64, i64, i32, ctypes.POINTER(i64), ctypes.c_char_p, i64]
     L.sys1hip_set_kernel.argtypes = [vp, i32]
     L.sys1hip_set_grid.argtypes = [vp, i32]
     L.sys1hip_set_dp_tiles.argtypes = [vp, i32]
@@ -97,7 +98,7 @@ def load() -> ctypes.CDLL:
                  "sys1hip_set_kernel", "sys1hip_set_grid", "sys1hip_set_dp_tiles",
                  "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
                  "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_kernel_count",
-                 "sys1hip_linear_bf16_noalloc", "sys1hip_pack_blocked_weight"):
+                 "sys1hip_linear_bf16_noalloc", "sys1hip_pack_blocked_weight", "sys1hip_plan_kernel"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -108,6 +109,16 @@ def check(code: int, ctx=None) -> int:
         msg = load().sys1hip_last_error(ctx)
         raise Sys1HipError(code, msg.decode() if msg else "")
     return code
+
+
+def plan_kernel(M: int, N: int, K: int, epilogue: int = 0, cus: int = 256) -> tuple[int, int, str]:
+    """(kernel id, workgroups, plan name) that the library would choose for a
+    projection on a GPU with `cus` compute units (no device needed)."""
+    L = load()
+    grid = ctypes.c_int64()
+    buf = ctypes.create_string_buffer(96)
+    kid = check(L.sys1hip_plan_kernel(cus, M, N, K, epilogue, ctypes.byref(grid), buf, 96))
+    return kid, grid.value, buf.value.decode()
 
 
 def kernel_names() -> list[str]:

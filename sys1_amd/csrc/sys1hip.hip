@@ -661,6 +661,32 @@ int sys1hip_sync(void* ctx) {
   return SYS1HIP_OK;
 }
 
+// The query above without a device: the fitted occupancies stand in for the
+// runtime's (the same numbers unless an epilogue variant spills).
+int sys1hip_plan_kernel(int32_t cus, int64_t M, int64_t N, int64_t K, int32_t epilogue, int64_t* grid,
+                        char* name, int64_t cap) {
+  if (cus <= 0) return fail(SYS1HIP_EINVAL, "sys1hip_plan_kernel: %d CUs", (int)cus);
+  if (epi_id_from_flags(epilogue) < 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_plan_kernel: unsupported epilogue flags %d", epilogue);
+  if (M <= 0 || N <= 0 || K <= 0) return fail(SYS1HIP_EINVAL, "sys1hip_plan_kernel: bad shape");
+  const int epi = epi_id_from_flags(epilogue);
+  if (epi_gated(epi) && N % (2 * SYS1HIP_GATE_GROUP) != 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_plan_kernel: gated N must be a multiple of %d", 2 * SYS1HIP_GATE_GROUP);
+  Context c;  // no device: cus and the fitted occupancies only
+  c.cus = cus;
+  const Plan p = price_plans(&c, M, N, K, K, epi, false, false);
+  if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_plan_kernel: no kernel fits this call");
+  if (grid) *grid = p.grid;
+  if (name && cap > 0) {
+    std::string s = kKernels[p.kernel].name;
+    s += "_g" + std::to_string(p.grid);
+    const int64_t tiles = cdiv(M, kKernels[p.kernel].bm) * cdiv(N, kKernels[p.kernel].bn);
+    if (kKernels[p.kernel].streamk && p.dp > 0 && p.dp < tiles) s += "_dp" + std::to_string(p.dp);
+    snprintf(name, (size_t)cap, "%s", s.c_str());
+  }
+  return p.kernel;
+}
+
 int sys1hip_set_kernel(void* ctx, int32_t id) {
   if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_set_kernel: null context");
   if (id < -1 || id >= kNumKernels)

@@ -1,0 +1,123 @@
+"""Host-side checks of the kernel chooser, without a device
+(sys1hip_plan_kernel prices the plans with the shapes' fitted occupancies).
+
+The first test pins the plans that the committed GPU measurements ran:
+- the ModernBERT-base chain (profiles/gemm_tile_256x160_p4_modernbert-base_kernel-trace.md);
+- the bench line's small-M object at M = 64 and 256
+  (profiles/skinny_modernbert-large_m64-m256_kernel-trace.md);
+- the Qwen3.5-27B weight stream at M = 128
+  (profiles/gemm_stream_128x128_qwen35-27b-m128_kernel-trace.md).
+
+A change of the cost model that moves them shows here first.  The rest are
+invariants over every projection shape of the four configurations and a
+sweep of packed M."""
+import re
+
+import pytest
+
+from sys1_amd import _lib
+from sys1_amd.stacks import CONFIGS
+
+E = _lib
+
+
+@pytest.mark.parametrize("M,N,K,epi,plan", [
+    # ModernBERT-base at the bench's mean ragged M
+    (8019, 2304, 768, E.EPI_NONE, "tile_256x160_s3_w8x1_p4_g256"),
+    (8019, 768, 768, E.EPI_RESIDUAL, "tile_128x192_s3_w4x2_p4_g252"),
+    (8019, 2304, 768, E.EPI_GEGLU, "tile_256x160_s3_w8x1_p4_g256"),
+    (8019, 768, 1152, E.EPI_RESIDUAL, "tile_128x192_s3_w4x2_p4_g252"),
+    # ModernBERT-large, small M: the skinny kernels
+    (64, 3072, 1024, E.EPI_NONE, "skinny_32x32_w16_g192"),
+    (64, 1024, 1024, E.EPI_RESIDUAL, "skinny_16x16_w16_g256"),
+    (64, 5248, 1024, E.EPI_GEGLU, "skinny_64x32_w16_g164"),
+    (64, 1024, 2624, E.EPI_RESIDUAL, "skinny_16x16_w16_g256"),
+    (256, 3072, 1024, E.EPI_NONE, "skinny_64x48_w8_g256"),
+    (256, 1024, 1024, E.EPI_RESIDUAL, "skinny_32x32_w16_g256"),
+    (256, 5248, 1024, E.EPI_GEGLU, "skinny_128x64_w4_g164"),
+    (256, 1024, 2624, E.EPI_RESIDUAL, "skinny_32x32_w16_g256"),
+    # Qwen3.5-27B at M = 128: weights streamed from HBM on the full stream-K grid
+    (128, 34816, 5120, E.EPI_SWIGLU, "stream_128x128_s4_w2x2_p4_g256_dp256"),
+    (128, 5120, 17408, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
+    (128, 16480, 5120, E.EPI_NONE, "stream_128x128_s4_w2x2_p4_g256"),
+])
+def test_plans_of_the_measured_workloads(M, N, K, epi, plan):
+    kid, grid, name = _lib.plan_kernel(M, N, K, epi)
+    assert name == plan
+    assert _lib.kernel_names()[kid] == re.sub(r"_g\d+(_dp\d+)?$", "", name)
+    assert grid == int(re.search(r"_g(\d+)", name).group(1))
+
+
+def _tile(name):
+    m = re.match(r"(tile|stream|skinny)_(\d+)x(\d+)_", name)
+    return m.group(1), int(m.group(2)), int(m.group(3))
+
+
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+def _shapes():
+    out = set()
+    for make in CONFIGS.values():
+        for layer in make().layers:
+            for p in layer:
+                out.add((p.N, p.K, p.epi))
+    return sorted(out)
+
+
+MS = [1, 7, 16, 64, 100, 128, 129, 256, 300, 1000, 1024, 4096, 4097, 8192, 16384]
+
+
+@pytest.mark.parametrize("N,K,epi", _shapes())
+def test_plan_invariants_over_m(N, K, epi):
+    """For every projection shape of the four configurations and a sweep of
+    M: the plan exists, its grid fits its schedule, and each family is used
+    in its regime (the chooser's documented rules)."""
+    names = _lib.kernel_names()
+    weight_bytes = 2 * N * K
+    for M in MS:
+        kid, grid, name = _lib.plan_kernel(M, N, K, epi)
+        kind, bm, bn = _tile(names[kid])
+        tiles = _cdiv(M, bm) * _cdiv(N, bn)
+        assert grid >= 1, (M, name)
+        if kind == "skinny":
+            # one workgroup per tile, one round over the CUs, small weights only
+            assert grid == tiles <= 256, (M, name)
+            assert M <= 4096 and weight_bytes <= 32 << 20, (M, name)
+        elif kind == "tile":
+            # a persistent tile grid: no more workgroups than tiles or slots
+            assert M > 128, (M, name)
+            assert grid <= tiles and grid <= 512, (M, name)
+        else:
+            # stream-K: at most one workgroup per (tile, k-tile) iteration
+            assert grid <= min(512, tiles * _cdiv(K, 64)), (M, name)
+        if epi in (E.EPI_GEGLU, E.EPI_SWIGLU) and kind == "skinny":
+            assert bn % 32 == 0, (M, name)  # whole gate/up row groups per workgroup
+
+
+def test_plans_follow_the_cu_count():
+    """Fewer CUs, no wider grid; the plan is deterministic."""
+    for M, N, K, epi in [(8019, 2304, 768, E.EPI_NONE), (128, 34816, 5120, E.EPI_SWIGLU),
+                         (64, 3072, 1024, E.EPI_NONE)]:
+        full = _lib.plan_kernel(M, N, K, epi, cus=256)
+        assert _lib.plan_kernel(M, N, K, epi, cus=256) == full
+        kid, grid, name = _lib.plan_kernel(M, N, K, epi, cus=64)
+        kind, bm, bn = _tile(_lib.kernel_names()[kid])
+        if kind != "skinny":
+            assert grid <= 64 * 2, name
+        else:
+            assert grid <= 64, name
+
+
+@pytest.mark.parametrize("args", [
+    (0, 64, 64, 64, 0),          # no CUs
+    (256, 0, 64, 64, 0),         # empty M (the linear call itself is a no-op; a plan is refused)
+    (256, 64, 64, -1, 0),        # bad K
+    (256, 64, 64, 64, 3),        # GeGLU | bias is not an epilogue
+    (256, 64, 48, 64, E.EPI_GEGLU),  # gated N not a multiple of 32
+])
+def test_plan_kernel_rejects_bad_arguments(args):
+    L = _lib.load()
+    assert L.sys1hip_plan_kernel(*args, None, None, 0) == _lib.EINVAL
+    assert L.sys1hip_last_error(None)
