@@ -6,6 +6,7 @@
 //   hipcc --offload-arch=gfx950 -O3 -std=c++17 -Xclang -target-feature \
 //         -Xclang -packed-fp32-ops sys1_amd/csrc/probes/pingpong_probe.hip -o /tmp/pingpong_probe
 //   /tmp/pingpong_probe [modes|epilogue|rotation|square]   (no argument: all)
+//   (run each GPU step under `timeout -k 10 120`)
 //
 // Kernel.  A workgroup computes a BM x BN output tile (BM tokens, BN output
 // features) with 4 NG waves in NG groups of four (group = wave / 4; waves are
@@ -29,7 +30,11 @@
 //   0  everything (the GEMM);
 //   1  no refills after the prologue (LDS reads and MFMAs on stale stages);
 //   2  no LDS reads and no refills (MFMAs and barriers only, on constant
-//      fragments: a data-dependent shader clock is not separated from it).
+//      fragments: a data-dependent shader clock is not separated from it);
+//   3  refills as in 0 but no LDS reads (MFMAs on constant fragments);
+//   4  LDS reads and refills as in 0, the refills from a 64-row window of
+//      x and of w (L2-resident after the first touch).
+// The shader clock printed with each timeline separates clock effects.
 // EPI_LDS: the epilogue stages the bf16 tile in LDS (two halves of BM / 2
 //   rows) and stores it with 16-byte row-contiguous lane accesses; otherwise
 //   each lane stores its 4 features of a block (8 bytes).
@@ -154,10 +159,12 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
       const int u = i * NW + wave;  // rows 16 u .. 16 u + 15 of [x rows; w rows]
       const int r = u * 16 + lrow;
       if (u < XT) {
-        src[i] = (unsigned)(min(m0 + r, M - 1) * K * 2 + ((lpos ^ swz4(r)) << 4));
+        const int row = MODE == 4 ? (r & 63) : m0 + r;
+        src[i] = (unsigned)(min(row, M - 1) * K * 2 + ((lpos ^ swz4(r)) << 4));
       } else {
         const int rw = r - BM;
-        src[i] = (unsigned)(min(n0 + rw, N - 1) * K * 2 + ((lpos ^ swz4(rw)) << 4));
+        const int row = MODE == 4 ? (rw & 63) : n0 + rw;
+        src[i] = (unsigned)(min(row, N - 1) * K * 2 + ((lpos ^ swz4(rw)) << 4));
       }
     }
     const int rot = ROT == 1 ? (3 * tn + 7 * tm) % U : 0;
@@ -208,14 +215,15 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
       // (its stage was last read before this group's previous compute
       // interval ended), then wait for this wave's share of unit u + 1.
       const char* sb = lds + (u % S) * kStage;
+      constexpr bool kReads = MODE != 2 && MODE != 3;
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
-        if (MODE != 2) fx[j] = *reinterpret_cast<const i32x4*>(sb + xaddr[j]);
+        if (kReads) fx[j] = *reinterpret_cast<const i32x4*>(sb + xaddr[j]);
         else asm volatile("" : "+v"(fx[j]));
       }
 #pragma unroll
       for (int i = 0; i < FN; ++i) {
-        if (MODE != 2) fw[i] = *reinterpret_cast<const i32x4*>(sb + waddr[i]);
+        if (kReads) fw[i] = *reinterpret_cast<const i32x4*>(sb + waddr[i]);
         else asm volatile("" : "+v"(fw[i]));
       }
       if (MODE != 1 && MODE != 2) {
@@ -410,6 +418,8 @@ int main(int argc, char** argv) {
     run<256, 288, 4, 3, 0, 4, true, 0>(8192, 2304, 768, true);
     run<256, 288, 4, 3, 1, 4, true, 0>(8192, 2304, 768, false);
     run<256, 288, 4, 3, 2, 4, true, 0>(8192, 2304, 768, false);
+    run<256, 288, 4, 3, 3, 4, true, 0>(8192, 2304, 768, false);
+    run<256, 288, 4, 3, 4, 4, true, 0>(8192, 2304, 768, false);
   }
   if (want("epilogue")) {
     run<256, 288, 4, 3, 0, 4, false, 0>(8192, 2304, 768, true);
@@ -423,6 +433,8 @@ int main(int argc, char** argv) {
     run<256, 256, 4, 2, 0, 4, true, 0>(8192, 8192, 8192, false);
     run<256, 256, 4, 2, 1, 4, true, 0>(8192, 8192, 8192, false);
     run<256, 256, 4, 2, 2, 4, true, 0>(8192, 8192, 8192, false);
+    run<256, 256, 4, 2, 3, 4, true, 0>(8192, 8192, 8192, false);
+    run<256, 256, 4, 2, 4, 4, true, 0>(8192, 8192, 8192, false);
   }
   return 0;
 }
