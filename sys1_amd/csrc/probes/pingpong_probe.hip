@@ -120,7 +120,8 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const int tiles = tiles_m * tiles_n;
   const int U = K / 32;  // (K % 32 == 0: checked on the host)
-  const rsrc_t xr = make_rsrc(x, 0x7ffffff0), wr = make_rsrc(w, 0x7ffffff0);
+  // Descriptor ranges end at the tensors: a read past them returns zeros.
+  const rsrc_t xr = make_rsrc(x, M * K * 2), wr = make_rsrc(w, N * K * 2);
   // Refill instruction i * NW + wave of a unit is this wave's; the last
   // round of instructions may not reach every wave.
   const bool full = wave + (kDmaMax - 1) * NW < DT;
