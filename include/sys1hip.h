@@ -141,6 +141,13 @@ SYS1HIP_API int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K,
 SYS1HIP_API int sys1hip_plan_kernel(int32_t cus, int64_t M, int64_t N, int64_t K, int32_t epilogue,
                         int64_t* grid, char* name, int64_t cap);
 
+/* The same with the call's leading dimensions (elements; ldw is ignored for
+ * a blocked weight): operands whose rows span 2 GiB or more from their base
+ * rule out the skinny kernels, whose buffer offsets are 32-bit.
+ * sys1hip_plan_kernel is this with ldx = ldw = K. */
+SYS1HIP_API int sys1hip_plan_kernel_strided(int32_t cus, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                        int64_t ldw, int32_t epilogue, int64_t* grid, char* name, int64_t cap);
+
 /* Force a kernel id for subsequent calls on this context (-1 = automatic
  * choice).  Used by the tile sweep and by tests that cover every kernel. */
 SYS1HIP_API int sys1hip_set_kernel(void* ctx, int32_t kernel_id);
@@ -246,12 +253,17 @@ SYS1HIP_API int sys1hip_set_dp_tiles(void* ctx, int32_t tiles);
  * kernel choice as sys1hip_linear_bf16, on the current HIP device, enqueued
  * on `stream` (a hipStream_t, NULL = the null stream).  Its stream-K
  * workspace is a static device array of 64 MB of partials plus 65536
- * arrival counters (64.25 MB in all), one per GPU, held from the first call
- * on that GPU until the process ends; the kernel plan is limited to that
- * workspace, and a call that would need more split tiles than there are
- * counters is refused (SYS1HIP_ERANGE).  The first call on a device looks
- * up the array's address and the kernels' occupancy (and clears the
- * counters when not under capture); it allocates nothing either.  Every call
+ * arrival counters (64.25 MB in all), one per GPU.  Being a file-scope
+ * __device__ array, it is allocated when the library's code object loads
+ * on a device and held until the process ends, for every user of the
+ * library on that device, whether or not it ever calls this entry point:
+ * count these 64.25 MB per GPU in the memory budget.  The kernel plan is
+ * limited to that workspace, and a call that would need more split tiles
+ * than there are counters is refused (SYS1HIP_ERANGE).  The first call on
+ * a device looks up the array's address and the kernels' occupancy (and
+ * clears the counters when not under capture); it allocates nothing
+ * either.  A set-up that fails returns the error and is tried again by the
+ * next call.  Every call
  * on one GPU shares that GPU's array: calls that overlap on one GPU (on
  * different streams, or from several threads) race on it and must not.
  * Errors: as sys1hip_linear_bf16, message from sys1hip_last_error(NULL). */

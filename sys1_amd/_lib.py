@@ -40,6 +40,7 @@ EXPORTS = (
     "sys1hip_set_dp_tiles", "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
     "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_linear_bf16_noalloc",
     "sys1hip_blocked_weight_bytes", "sys1hip_pack_blocked_weight", "sys1hip_plan_kernel",
+    "sys1hip_plan_kernel_strided",
 )
 
 
@@ -81,6 +82,8 @@ def load() -> ctypes.CDLL:
     L.sys1hip_pack_blocked_weight.argtypes = [vp, vp, i64, vp, i64, i64]
     L.sys1hip_query_kernel.argtypes = [vp, i64, i64, i64, i32, ctypes.c_char_p, i64]
     L.sys1hip_plan_kernel.argtypes = [i32, i64, i64, i64, i32, ctypes.POINTER(i64), ctypes.c_char_p, i64]
+    L.sys1hip_plan_kernel_strided.argtypes = [i32, i64, i64, i64, i64, i64, i32, ctypes.POINTER(i64),
+                                              ctypes.c_char_p, i64]
     L.sys1hip_set_kernel.argtypes = [vp, i32]
     L.sys1hip_set_grid.argtypes = [vp, i32]
     L.sys1hip_set_dp_tiles.argtypes = [vp, i32]
@@ -98,7 +101,8 @@ def load() -> ctypes.CDLL:
                  "sys1hip_set_kernel", "sys1hip_set_grid", "sys1hip_set_dp_tiles",
                  "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
                  "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_kernel_count",
-                 "sys1hip_linear_bf16_noalloc", "sys1hip_pack_blocked_weight", "sys1hip_plan_kernel"):
+                 "sys1hip_linear_bf16_noalloc", "sys1hip_pack_blocked_weight", "sys1hip_plan_kernel",
+                 "sys1hip_plan_kernel_strided"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -111,13 +115,16 @@ def check(code: int, ctx=None) -> int:
     return code
 
 
-def plan_kernel(M: int, N: int, K: int, epilogue: int = 0, cus: int = 256) -> tuple[int, int, str]:
+def plan_kernel(M: int, N: int, K: int, epilogue: int = 0, cus: int = 256,
+                ldx: int | None = None, ldw: int | None = None) -> tuple[int, int, str]:
     """(kernel id, workgroups, plan name) that the library would choose for a
-    projection on a GPU with `cus` compute units (no device needed)."""
+    projection on a GPU with `cus` compute units (no device needed); ldx /
+    ldw default to K (contiguous rows)."""
     L = load()
     grid = ctypes.c_int64()
     buf = ctypes.create_string_buffer(96)
-    kid = check(L.sys1hip_plan_kernel(cus, M, N, K, epilogue, ctypes.byref(grid), buf, 96))
+    kid = check(L.sys1hip_plan_kernel_strided(cus, M, N, K, ldx or K, ldw or K, epilogue,
+                                              ctypes.byref(grid), buf, 96))
     return kid, grid.value, buf.value.decode()
 
 

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -57,7 +58,7 @@ struct PlanKey {
   int64_t M, N, K;
   int epi;
   bool head64, conv;
-  bool wide_w;  // weight rows span 2 GiB or more (the skinny kernels' offsets would not reach)
+  bool wide_w;  // x or w spans 2 GiB or more (the skinny kernels' offsets would not reach: skinny_wide)
   bool operator==(const PlanKey& o) const {
     return M == o.M && N == o.N && K == o.K && epi == o.epi && head64 == o.head64 && conv == o.conv &&
            wide_w == o.wide_w;
@@ -333,8 +334,15 @@ constexpr int64_t kSkinnyMaxM = 4096;
 constexpr int64_t kSkinnyWeightBytes = 32 << 20;
 constexpr int64_t kSkinnyCuBytes = 512 << 10;
 
-int skinny_pick(const Context* c, int64_t M, int64_t N, int64_t K, int64_t ldw, int epi) {
-  if (M > kSkinnyMaxM || 2 * N * K > kSkinnyWeightBytes || 2 * N * ldw >= 0x7ffffff0ll) return -1;
+// The skinny kernels address x and w through one buffer descriptor each,
+// based at row 0, with 32-bit byte offsets: a call whose operands span 2 GiB
+// or more from there (a strided x view, a huge weight) cannot run on them.
+bool skinny_wide(int64_t M, int64_t K, int64_t ldx, int64_t N, int64_t ldw) {
+  return 2 * (M - 1) * ldx + 2 * K >= 0x7ffffff0ll || 2 * N * ldw >= 0x7ffffff0ll;
+}
+
+int skinny_pick(const Context* c, int64_t M, int64_t N, int64_t K, bool wide, int epi) {
+  if (M > kSkinnyMaxM || 2 * N * K > kSkinnyWeightBytes || wide) return -1;
   int best = -1;
   int64_t best_bytes = 0;
   for (int id = 0; id < kNumKernels; ++id) {
@@ -347,12 +355,12 @@ int skinny_pick(const Context* c, int64_t M, int64_t N, int64_t K, int64_t ldw, 
   return best >= 0 && best_bytes <= kSkinnyCuBytes ? best : -1;
 }
 
-Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int64_t ldw, int epi, bool head64,
+Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, bool wide, int epi, bool head64,
                  bool conv) {
   Plan best;
   // (a forced grid or split asks for a persistent kernel: no skinny pick)
   if (c->forced_kernel < 0 && c->forced_grid <= 0 && c->forced_dp < 0 && !head64 && !conv) {
-    const int id = skinny_pick(c, M0, N, K, ldw, epi);
+    const int id = skinny_pick(c, M0, N, K, wide, epi);
     if (id >= 0) {
       best.kernel = id, best.grid = cdiv(M0, kKernels[id].bm) * cdiv(N, kKernels[id].bn), best.dp = 0,
       best.cost = 0.0;
@@ -366,7 +374,7 @@ Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int64_t ldw
     if (e.skinny) {
       // (only when forced: the automatic choice is skinny_pick's; the grid
       // is one workgroup per tile, whatever grid is forced)
-      if (c->forced_kernel != id || head64 || conv || 2 * N * ldw >= 0x7ffffff0ll) continue;
+      if (c->forced_kernel != id || head64 || conv || wide) continue;
       best.kernel = id, best.grid = cdiv(M0, e.bm) * cdiv(N, e.bn), best.dp = 0, best.cost = 0.0;
       continue;
     }
@@ -418,16 +426,16 @@ Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, int64_t ldw
 // sees many distinct M).
 constexpr size_t kPlanCacheMax = 1 << 14;
 
-Plan resolve(Context* c, int64_t M0, int64_t N, int64_t K, int64_t ldw, int epi, bool head64 = false,
+Plan resolve(Context* c, int64_t M0, int64_t N, int64_t K, bool wide, int epi, bool head64 = false,
              bool conv = false) {
   if (c->forced_kernel >= 0 || c->forced_grid > 0 || c->forced_dp >= 0)
-    return price_plans(c, M0, N, K, ldw, epi, head64, conv);
-  const PlanKey key{M0, N, K, epi, head64, conv, 2 * N * ldw >= 0x7ffffff0ll};
+    return price_plans(c, M0, N, K, wide, epi, head64, conv);
+  const PlanKey key{M0, N, K, epi, head64, conv, wide};
   std::lock_guard<std::mutex> lock(c->plan_mu);
   auto it = c->plans.find(key);
   if (it != c->plans.end()) return it->second;
   if (c->plans.size() >= kPlanCacheMax) c->plans.clear();
-  const Plan p = price_plans(c, M0, N, K, ldw, epi, head64, conv);
+  const Plan p = price_plans(c, M0, N, K, wide, epi, head64, conv);
   c->plans.emplace(key, p);
   return p;
 }
@@ -665,6 +673,12 @@ int sys1hip_sync(void* ctx) {
 // runtime's (the same numbers unless an epilogue variant spills).
 int sys1hip_plan_kernel(int32_t cus, int64_t M, int64_t N, int64_t K, int32_t epilogue, int64_t* grid,
                         char* name, int64_t cap) {
+  return sys1hip_plan_kernel_strided(cus, M, N, K, K, K, epilogue, grid, name, cap);
+}
+
+int sys1hip_plan_kernel_strided(int32_t cus, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
+                                int32_t epilogue, int64_t* grid, char* name, int64_t cap) {
+  if (ldx < K || ldw < K) return fail(SYS1HIP_EINVAL, "sys1hip_plan_kernel: ldx/ldw below K");
   if (cus <= 0) return fail(SYS1HIP_EINVAL, "sys1hip_plan_kernel: %d CUs", (int)cus);
   if (epi_id_from_flags(epilogue) < 0)
     return fail(SYS1HIP_EINVAL, "sys1hip_plan_kernel: unsupported epilogue flags %d", epilogue);
@@ -674,7 +688,7 @@ int sys1hip_plan_kernel(int32_t cus, int64_t M, int64_t N, int64_t K, int32_t ep
     return fail(SYS1HIP_EINVAL, "sys1hip_plan_kernel: gated N must be a multiple of %d", 2 * SYS1HIP_GATE_GROUP);
   Context c;  // no device: cus and the fitted occupancies only
   c.cus = cus;
-  const Plan p = price_plans(&c, M, N, K, K, epi, false, false);
+  const Plan p = price_plans(&c, M, N, K, skinny_wide(M, K, ldx, N, plan_ldw(ldw, K, epilogue)), epi, false, false);
   if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_plan_kernel: no kernel fits this call");
   if (grid) *grid = p.grid;
   if (name && cap > 0) {
@@ -717,7 +731,7 @@ int sys1hip_query_kernel(void* ctx, int64_t M, int64_t N, int64_t K, int32_t epi
   Context* c = static_cast<Context*>(ctx);
   if (M <= 0 || N <= 0 || K <= 0)
     return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: bad shape");
-  const Plan p = resolve(c, M, N, K, K, epi_id_from_flags(epilogue));
+  const Plan p = resolve(c, M, N, K, skinny_wide(M, K, K, N, K), epi_id_from_flags(epilogue));
   const int id = p.kernel;
   if (id < 0) return fail(SYS1HIP_EINVAL, "sys1hip_query_kernel: the forced kernel does not fit this call");
   if (name && cap > 0) {
@@ -740,7 +754,7 @@ int sys1hip_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const uint16_
   rc = use_device(c);
   if (rc) return rc;
   const int epi = epi_id_from_flags(epilogue);
-  return launch_linear("sys1hip_linear_bf16", c, resolve(c, M, N, K, plan_ldw(ldw, K, epilogue), epi), c->stream,
+  return launch_linear("sys1hip_linear_bf16", c, resolve(c, M, N, K, skinny_wide(M, K, ldx, N, plan_ldw(ldw, K, epilogue)), epi), c->stream,
                        c->ws, c->counters, x, ldx, w, ldw, bias, residual, ldr, y, ldy, M, N, K, epi,
                        epilogue & SYS1HIP_EPI_BLOCKED_W);
 }
@@ -769,7 +783,8 @@ __global__ void clear_words_kernel(unsigned* p, int64_t n) {
 // Per device: the scratch address and the plan inputs (CU count and the
 // kernels' occupancy), all in static storage.
 struct StaticDevice {
-  std::once_flag once;
+  std::mutex mu;      // guards the set-up; `ready` is set only when it succeeded,
+  std::atomic<bool> ready{false};  // so a failed set-up is retried by the next call
   int rc = SYS1HIP_OK;
   char* ptr = nullptr;
   Context plan_ctx;  // only cus and occ_fixed are used (price_plans)
@@ -823,12 +838,20 @@ int sys1hip_linear_bf16_noalloc(void* stream, const uint16_t* x, int64_t ldx, co
     return fail(SYS1HIP_EDEVICE, "%s: device %d beyond the %d this entry point serves", who, dev, kMaxStaticDevices);
   StaticDevice& d = g_static[dev];
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  std::call_once(d.once, [&] { d.rc = setup_static(d, dev, s); });
-  if (d.rc) return fail(d.rc, "%s: set-up on device %d failed", who, dev);
+  if (!d.ready.load(std::memory_order_acquire)) {
+    std::lock_guard<std::mutex> lock(d.mu);
+    if (!d.ready.load(std::memory_order_relaxed)) {
+      d.rc = setup_static(d, dev, s);
+      if (d.rc) return fail(d.rc, "%s: set-up on device %d failed (retried on the next call): %s", who, dev,
+                            g_last_error.c_str());
+      d.ready.store(true, std::memory_order_release);
+    }
+  }
   // The plan is priced on every call (no cache: a cache insert would
   // allocate host memory).
   const int epi = epi_id_from_flags(epilogue);
-  const Plan p = price_plans(&d.plan_ctx, M, N, K, plan_ldw(ldw, K, epilogue), epi, false, false);
+  const Plan p = price_plans(&d.plan_ctx, M, N, K, skinny_wide(M, K, ldx, N, plan_ldw(ldw, K, epilogue)), epi,
+                             false, false);
   return launch_linear(who, &d.plan_ctx, p, s, reinterpret_cast<float*>(d.ptr),
                        reinterpret_cast<unsigned*>(d.ptr + kWorkspaceBytes), x, ldx, w, ldw, bias, residual, ldr,
                        y, ldy, M, N, K, epi, epilogue & SYS1HIP_EPI_BLOCKED_W);
@@ -864,7 +887,7 @@ int sys1hip_linear_rope_qkv_bf16(void* ctx, const uint16_t* x, int64_t ldx, cons
   if (c->forced_kernel >= 0 && kKernels[c->forced_kernel].tn != 64)
     return fail(SYS1HIP_EINVAL, "sys1hip_linear_rope_qkv_bf16: forced kernel %s is not head-aligned",
                 kKernels[c->forced_kernel].name);
-  const Plan p = resolve(c, M, N, K, ldw, kEpiRopeQkv, true);
+  const Plan p = resolve(c, M, N, K, skinny_wide(M, K, ldx, N, ldw), kEpiRopeQkv, true);
   if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_linear_rope_qkv_bf16: the forced kernel does not fit this call");
   const KernelEntry& e = kKernels[p.kernel];
   if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
@@ -983,7 +1006,7 @@ int sys1hip_norm_linear_bf16(void* ctx, const uint16_t* x, int64_t ldx, const ui
     return fail(SYS1HIP_ERANGE, "sys1hip_norm_linear_bf16: dimension above 2^30");
   int rc = use_device(c);
   if (rc) return rc;
-  const Plan p = resolve(c, M, N, K, plan_ldw(ldw, K, epilogue), epi);
+  const Plan p = resolve(c, M, N, K, skinny_wide(M, K, ldx, N, plan_ldw(ldw, K, epilogue)), epi);
   if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_norm_linear_bf16: the forced kernel does not fit this call");
   const KernelEntry& e = kKernels[p.kernel];
   if (e.streamk && (cdiv(M, e.bm) * cdiv(N, e.bn) - p.dp) * (e.threads / 64) > kCounterSlots)
@@ -1061,7 +1084,7 @@ int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx, con
   // shapes lose more in the GEMM than the fused form saves in traffic.
   const bool fused = c->forced_kernel >= 0 && kKernels[c->forced_kernel].wm == 1;
   const int epi = fused ? (norm ? kEpiNormRmsConvSilu : kEpiConvSilu) : (norm ? kEpiNormRms : kEpiNone);
-  const Plan p = resolve(c, M, N, K, ldw, epi, false, fused);
+  const Plan p = resolve(c, M, N, K, skinny_wide(M, K, ldx, N, ldw), epi, false, fused);
   if (p.kernel < 0) return fail(SYS1HIP_EINVAL, "sys1hip_linear_conv_silu_bf16: the forced kernel does not fit this call");
   const KernelEntry& e = kKernels[p.kernel];
   if (!e.fn[epi])

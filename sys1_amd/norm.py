@@ -22,7 +22,7 @@ import torch
 
 from . import _lib
 from .device import HipDevice, load as load_device
-from .linear import _check_operand, _rows, pack_gated_weight
+from .linear import _check_operand, _rows, pack_blocked_weight, pack_gated_weight
 
 _vp = ctypes.c_void_p
 KINDS = {"layer": _lib.NORM_LAYER, "rms": _lib.NORM_RMS}
@@ -55,10 +55,12 @@ class NormLinear:
     weight: [N, K] bf16 ([out, in]); for gated=... [2I, K] with the gate rows
     first.  gamma: the norm's weight [K] (LayerNorm weight, or the RMSNorm
     weight w of alpha = 1 + w).  kind: "layer" or "rms".  gated: None,
-    "gelu" (GeGLU, with LayerNorm) or "silu" (SwiGLU, with RMSNorm)."""
+    "gelu" (GeGLU, with LayerNorm) or "silu" (SwiGLU, with RMSNorm).
+    blocked=True stores the folded weight in the blocked layout
+    (pack_blocked_weight); the results are those of the row-major weight."""
 
     def __init__(self, weight: torch.Tensor, gamma: torch.Tensor, kind: str, eps: float,
-                 gated: str | None = None, device: HipDevice | None = None):
+                 gated: str | None = None, device: HipDevice | None = None, blocked: bool = False):
         self.device = device or load_device(weight.device.index or 0)
         if kind not in KINDS:
             raise ValueError(f"norm kind must be one of {sorted(KINDS)}, got {kind!r}")
@@ -68,6 +70,10 @@ class NormLinear:
         self.kind, self.eps, self.epilogue = kind, float(eps), epi
         w = pack_gated_weight(weight, self.device) if gated else weight
         self.weight, self.colsum = fold_norm_weight(w, gamma, kind, self.device)
+        self.rows = self.weight.shape[0]
+        self.blocked = blocked
+        if blocked:  # fold (and gate/up interleave) first, then the blocked layout of that
+            self.weight = pack_blocked_weight(self.weight, self.device)
         self.in_features = weight.shape[1]
         self.out_features = weight.shape[0] // 2 if gated else weight.shape[0]
 
@@ -84,11 +90,11 @@ class NormLinear:
         dev.follow_torch_stream()
         _lib.check(dev._L.sys1hip_norm_linear_bf16(
             dev.ctx, _vp(x2.data_ptr()), x2.stride(0) if M > 1 else K,
-            _vp(self.weight.data_ptr()), self.weight.stride(0),
+            _vp(self.weight.data_ptr()), K if self.blocked else self.weight.stride(0),
             _vp(self.colsum.data_ptr()) if self.colsum is not None else None,
             KINDS[self.kind], self.eps,
             _vp(o2.data_ptr()), o2.stride(0) if M > 1 else o2.shape[1],
-            M, self.weight.shape[0], K, self.epilogue), dev.ctx)
+            M, self.rows, K, self.epilogue | (_lib.EPI_BLOCKED_W if self.blocked else 0)), dev.ctx)
         return out
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

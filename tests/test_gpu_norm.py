@@ -192,3 +192,38 @@ def test_norm_linear_errors(dev, orc):
     with pytest.raises(_lib.Sys1HipError):
         NormLinear(torch.zeros(64, 64, dtype=torch.bfloat16, device="cuda:0"), g, "rms", 1e-6,
                    "gelu", device=dev)(torch.zeros(4, 64, dtype=torch.bfloat16, device="cuda:0"))
+
+
+def test_blocked_weight_with_every_norm_epilogue_is_bitwise_row_major(dev, orc):
+    """The folded weight in the blocked layout (what ProjectionStack(norms=True,
+    blocked=True) and the bench run) gives the row-major folded weight's
+    results bit for bit, on a forced kernel of every family (tile, stream-K,
+    skinny) and every pre-norm epilogue, with N and K not multiples of the
+    32 x 64 block."""
+    from sys1_amd import kernel_names
+    from sys1_amd.norm import NormLinear
+    names = kernel_names()
+    picks = [next(i for i, n in enumerate(names) if n.startswith(f)) for f in ("tile_", "stream_", "skinny_")]
+    picks += [i for i, n in enumerate(names) if n.startswith("skinny_") and int(n.split("_")[1].split("x")[1]) % 32 == 0][:1]
+    M, N, K = 150, 352, 328
+    x = _stream(orc, M, K, 41)
+    xg = to_gpu_bf16(x, torch)
+    try:
+        for kind, gated in (("layer", None), ("layer", "gelu"), ("rms", None), ("rms", "silu")):
+            eps = 1e-5 if kind == "layer" else 1e-6
+            w, g = _weights(orc, N, K, 43, kind)
+            wg, gg = to_gpu_bf16(w, torch), torch.from_numpy(g)
+            rm = NormLinear(wg, gg, kind, eps, gated, device=dev)
+            bl = NormLinear(wg, gg, kind, eps, gated, device=dev, blocked=True)
+            ref = _ref(orc, x, w, g, kind, eps, gated)
+            for kid in picks:
+                name = names[kid]
+                if gated and name.startswith("skinny_") and int(name.split("_")[1].split("x")[1]) % 32:
+                    continue
+                dev.set_kernel(kid)
+                print(f"[gpu] blocked norm {name} {kind}/{gated}", flush=True)
+                a, b = rm(xg), bl(xg)
+                assert torch.equal(a, b), f"{name} {kind}/{gated}"
+                assert_parity(to_np(b), ref, f"blocked {name} {kind}/{gated}")
+    finally:
+        dev.set_kernel(-1)

@@ -557,3 +557,54 @@ def test_qwen_stack_with_norms_and_conv_matches_f32_chain(dev, orc):
     rel, mx = parity(h_gpu, h)
     print(f"[gpu] qwen norms+conv final hidden vs f32 chain: rel_fro={rel:.3e} max={mx:.3e}", flush=True)
     assert rel < CHAIN_TOL and mx < 5 * CHAIN_TOL
+
+
+def test_bench_stack_object_at_cfg2_size(dev, orc):
+    """The object bench.py times, at its size: ProjectionStack(blocked=True)
+    over all 22 ModernBERT-base layers on a config-2 ragged batch (lengths
+    U[16,512] packed to 8192).  Its prepared calls run one at a time; every
+    projection's output is checked against the oracle's f32 projection of
+    the input (and residual) the GPU chain actually fed it, and the whole
+    stack enqueued at once (as the bench does) must give the same bits.
+    The stack has no norms (they are not projections), so the hidden state
+    grows layer over layer; the final state is compared with the oracle
+    chain that rounds where the GPU path rounds, and reported."""
+    from sys1_amd.batching import draw_lengths
+    from sys1_amd.stacks import CONFIGS, ProjectionStack
+    cfg = CONFIGS["modernbert-base"]()
+    M = int(draw_lengths(11, 16, 512, 8192).sum())
+    print(f"[gpu] bench stack object: modernbert-base 22 layers blocked M={M}", flush=True)
+    x = orc.fill_normal((M, 768), 29)
+    ws = _weights(orc, cfg, 300)
+    xg = to_gpu_bf16(x, torch)
+    stack = ProjectionStack(cfg, dev, M, weights=[[to_gpu_bf16(w, torch) for w in l] for l in ws],
+                            blocked=True)
+    prepared = stack.prepare(xg, M)
+    assert len(prepared) == 4 * 22
+    bufs = stack.buffers
+    h_prev = xg  # the residual source of the first output projection is x itself
+    worst = 0.0
+    dev.follow_torch_stream()
+    for i, (p, fn, args) in enumerate(prepared):
+        li = i // 4
+        src = xg if (p.src == "h" and i == 0) else (bufs[p.src][:M, p.src_off:p.src_off + p.K]
+                                                    if p.src != "h" else bufs["h"][:M, :768])
+        src_np = to_np(src)
+        resid_np = to_np(h_prev) if p.resid else None
+        stack.run_prepared([(p, fn, args)])
+        torch.cuda.synchronize()
+        out = bufs[p.dst][:M, :p.nout]
+        ref = _project_ref(orc, p, src_np, ws[li][i % 4], resid_np)
+        rel, _ = assert_parity(to_np(out), ref, f"layer {li} {p.name} M={M}")
+        worst = max(worst, rel)
+        if p.dst == "h":
+            h_prev = bufs["h"][:M, :768].clone()
+    step_by_step = bufs["h"][:M, :768].clone()
+    once = stack.forward(xg, M).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(step_by_step, once)
+    emul = _oracle_chain_bf16(orc, cfg, x, ws, None)
+    rel, _ = parity(to_np(once), emul)
+    print(f"[gpu] bench stack object: worst per-projection rel_fro {worst:.3e}; final hidden vs the "
+          f"bf16-rounding oracle chain rel_fro {rel:.3e}", flush=True)
+    assert rel < 5e-2

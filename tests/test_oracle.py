@@ -419,3 +419,119 @@ def test_rope_tables_and_invariants(orc):
         b = out[plane].reshape(7, heads, 2, half)
         np.testing.assert_allclose(np.hypot(a[:, :, 0], a[:, :, 1]), np.hypot(b[:, :, 0], b[:, :, 1]),
                                    rtol=2e-5, atol=1e-5)
+
+
+# ------------------------------------------------------- composite chains ---
+
+def _torch_scorer_f64(h, ln_w, ln_b, w_in, b_in, w_out, b_out):
+    """Independent restatement through torch f64 library calls:
+    layer_norm -> addmm -> gelu(erf) -> addmm (src/models/laya.rs:510-520)."""
+    import torch
+    t = lambda a: torch.from_numpy(np.asarray(a, np.float64))
+    z = torch.nn.functional.layer_norm(t(h), (h.shape[1],), t(ln_w), t(ln_b), 1e-5)
+    z = torch.nn.functional.gelu(torch.addmm(t(b_in), z, t(w_in).T), approximate="none")
+    return torch.addmm(t(b_out), z, t(w_out).T)[:, 0].numpy()
+
+
+def test_laya_scorer_against_torch_f64(orc):
+    rng = np.random.default_rng(5)
+    H = 96
+    h = orc.fill_normal((37, H), 3)
+    ln_w = (1 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    ln_b = (0.1 * rng.standard_normal(H)).astype(np.float32)
+    w_in = orc.fill_normal((H, H), 4, 0.1)
+    b_in = (0.1 * rng.standard_normal(H)).astype(np.float32)
+    w_out = orc.fill_normal((1, H), 6, 0.1)
+    b_out = np.array([0.25], np.float32)
+    got = orc.laya_scorer_f32(h, ln_w, ln_b, w_in, b_in, w_out, b_out)
+    ref = _torch_scorer_f64(h, ln_w, ln_b, w_in, b_in, w_out, b_out)
+    assert got.shape == (37,)
+    assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+    # A GELU applied before the bias (a plausible slip) moves the logits well
+    # beyond that bound: the bias is large enough to matter.
+    wrong = _torch_scorer_f64(h, ln_w, ln_b, w_in, 0 * b_in, w_out, b_out)
+    assert np.abs(wrong - ref).max() > 1e-3
+
+
+def test_laya_scorer_closed_forms(orc):
+    H = 64
+    rng = np.random.default_rng(9)
+    h = orc.fill_normal((5, H), 8)
+    ln_w = np.ones(H, np.float32)
+    ln_b = np.zeros(H, np.float32)
+    b_in = rng.standard_normal(H).astype(np.float32)
+    w_out = rng.standard_normal((1, H)).astype(np.float32)
+    b_out = np.array([-0.75], np.float32)
+    # Zero w_in: every row gives gelu(b_in) . w_out + b_out, whatever h is.
+    got = orc.laya_scorer_f32(h, ln_w, ln_b, np.zeros((H, H), np.float32), b_in, w_out, b_out)
+    gel = 0.5 * b_in.astype(np.float64) * (1 + np.array([math.erf(v / math.sqrt(2)) for v in b_in]))
+    want = float(gel @ w_out[0].astype(np.float64) + b_out[0])
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-5)
+    # Identity w_in, zero biases and LN weight 1: logit = sum_k gelu(ln(h)_k) w_out[k];
+    # with ln_b = 0 the normalised row has mean 0 and variance 1 (eps aside).
+    got = orc.laya_scorer_f32(h, ln_w, ln_b, np.eye(H, dtype=np.float32), np.zeros(H, np.float32),
+                              w_out, np.zeros(1, np.float32))
+    hd = h.astype(np.float64)
+    z = (hd - hd.mean(1, keepdims=True)) / np.sqrt(hd.var(1, keepdims=True) + 1e-5)
+    gz = 0.5 * z * (1 + scipy.special.erf(z / math.sqrt(2)))
+    assert np.allclose(got, gz @ w_out[0], rtol=1e-5, atol=1e-5)
+    # The LayerNorm is applied: scaling a row (LN is scale-invariant up to eps)
+    # leaves its logit, while a row shift leaves it too (mean removed).
+    base = orc.laya_scorer_f32(h, ln_w, ln_b, np.eye(H, dtype=np.float32), b_in, w_out, b_out)
+    moved = orc.laya_scorer_f32((3 * h + 2).astype(np.float32), ln_w, ln_b, np.eye(H, dtype=np.float32),
+                                b_in, w_out, b_out)
+    assert np.allclose(base, moved, rtol=1e-4, atol=1e-4)
+
+
+def _mb_weights(orc, H, I, seed):
+    return [orc.fill_normal((3 * H, H), seed, 0.05), orc.fill_normal((H, H), seed + 1, 0.05),
+            orc.fill_normal((2 * I, H), seed + 2, 0.05), orc.fill_normal((H, I), seed + 3, 0.05)]
+
+
+def test_modernbert_layer_against_numpy_f64(orc):
+    """The layer chain of src/archs/modernbert.rs:857-887 (with the V-block
+    attention stand-in) restated in numpy f64: Wqkv -> V block -> Wo + h ->
+    Wi -> gelu(first half) * second half -> Wo + h1."""
+    H, I = 32, 48
+    h = orc.fill_normal((19, H), 2)
+    wqkv, wo, wi, wo2 = _mb_weights(orc, H, I, 20)
+    d = lambda a: np.asarray(a, np.float64)
+    qkv = d(h) @ d(wqkv).T
+    h1 = qkv[:, 2 * H:] @ d(wo).T + d(h)
+    u = h1 @ d(wi).T
+    g = 0.5 * u[:, :I] * (1 + scipy.special.erf(u[:, :I] / math.sqrt(2))) * u[:, I:]
+    ref = g @ d(wo2).T + h1
+    got = orc.modernbert_layer_f32(h, wqkv, wo, wi, wo2)
+    assert got.shape == h.shape
+    assert _rel_fro(got, ref) < 1e-5
+
+
+def test_modernbert_layer_closed_forms(orc):
+    H, I = 16, 24
+    h = orc.fill_normal((7, H), 4)
+    wqkv, wo, wi, wo2 = _mb_weights(orc, H, I, 30)
+    z = lambda a: np.zeros_like(a)
+    # All weights zero: both residuals carry h through unchanged, exactly.
+    assert np.array_equal(orc.modernbert_layer_f32(h, z(wqkv), z(wo), z(wi), z(wo2)), h)
+    # A one-hot V block (rows 2H.. of Wqkv = I) with Wo = I and the MLP off:
+    # out = h + V = 2h.  The same one-hot placed in the q or k block gives h.
+    eye = np.eye(H, dtype=np.float32)
+    for blk, want in ((2, 2 * h), (0, h), (1, h)):
+        w = np.zeros((3 * H, H), np.float32)
+        w[blk * H:(blk + 1) * H] = eye
+        got = orc.modernbert_layer_f32(h, w, eye, z(wi), z(wo2))
+        assert np.allclose(got, want, rtol=0, atol=1e-6), blk
+    # Each residual alone: attention branch off (Wo = 0) leaves h + MLP(h);
+    # MLP off leaves h + attention(h).
+    d = lambda a: np.asarray(a, np.float64)
+    u = d(h) @ d(wi).T
+    mlp = (0.5 * u[:, :I] * (1 + scipy.special.erf(u[:, :I] / math.sqrt(2))) * u[:, I:]) @ d(wo2).T
+    got = orc.modernbert_layer_f32(h, wqkv, z(wo), wi, wo2)
+    assert _rel_fro(got, d(h) + mlp) < 1e-5
+    attn = (d(h) @ d(wqkv).T)[:, 2 * H:] @ d(wo).T
+    got = orc.modernbert_layer_f32(h, wqkv, wo, z(wi), wo2)
+    assert _rel_fro(got, d(h) + attn) < 1e-5
+    # The gate is the first half of Wi's output: swapping the halves changes it.
+    swapped = np.concatenate([wi[I:], wi[:I]])
+    mlp_of = lambda w: orc.modernbert_layer_f32(h, wqkv, z(wo), w, wo2).astype(np.float64) - h
+    assert _rel_fro(mlp_of(swapped), mlp_of(wi)) > 0.5

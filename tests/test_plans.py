@@ -121,3 +121,20 @@ def test_plan_kernel_rejects_bad_arguments(args):
     L = _lib.load()
     assert L.sys1hip_plan_kernel(*args, None, None, 0) == _lib.EINVAL
     assert L.sys1hip_last_error(None)
+
+
+def test_strided_x_beyond_2gib_rules_out_the_skinny_kernels():
+    """The skinny kernels address x from row 0 with 32-bit byte offsets: an x
+    view whose rows span 2 GiB or more (a large leading dimension) must get
+    a tile or stream-K plan, and so must a weight that wide; the same shape
+    with contiguous rows stays skinny."""
+    M, N, K = 64, 1024, 1024
+    _, _, plain = E.plan_kernel(M, N, K, E.EPI_NONE)
+    assert plain.startswith("skinny_")
+    ldx = (1 << 31) // (2 * (M - 1)) + 8  # 2 (M-1) ldx >= 2 GiB
+    _, _, wide = E.plan_kernel(M, N, K, E.EPI_NONE, ldx=ldx)
+    assert not wide.startswith("skinny_"), wide
+    _, _, just = E.plan_kernel(M, N, K, E.EPI_NONE, ldx=(0x7ffffff0 - 2 * K) // (2 * (M - 1)) - 8)
+    assert just.startswith("skinny_"), just
+    _, _, wide_w = E.plan_kernel(M, N, K, E.EPI_NONE, ldw=(1 << 31) // (2 * N) + 8)
+    assert not wide_w.startswith("skinny_"), wide_w

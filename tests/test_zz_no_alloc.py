@@ -103,3 +103,59 @@ def test_noalloc_under_graph_capture(orc):
             _lib.check(_call(L, L.sys1hip_linear_bf16_noalloc, s, x2, w, y_other, res=res, epi=epi))
             torch.cuda.synchronize()
         del g
+
+
+_FIRST_CALL_UNDER_CAPTURE = r"""
+import ctypes, sys
+import torch
+sys.path.insert(0, sys.argv[1])
+from sys1_amd import _lib
+L = _lib.load()
+torch.manual_seed(0)
+M, N, K = 64, 8192, 4096  # a stream-K plan: the static workspace and its counters
+x = torch.randn(M, K).to(torch.bfloat16).cuda()
+w = (torch.randn(N, K) * 0.02).to(torch.bfloat16).cuda()
+r = torch.randn(M, N).to(torch.bfloat16).cuda()
+y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+p = lambda t: ctypes.c_void_p(t.data_ptr())
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = L.sys1hip_linear_bf16_noalloc(s, p(x), K, p(w), K, None, p(r), N, p(y), N, M, N, K, _lib.EPI_RESIDUAL)
+print("first call under capture: rc", rc, flush=True)
+assert rc == 0, L.sys1hip_last_error(None)
+from sys1_amd.device import HipDevice
+dev = HipDevice(0)
+ref = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+dev.follow_torch_stream()
+_lib.check(L.sys1hip_linear_bf16(dev.ctx, p(x), K, p(w), K, None, p(r), N, p(ref), N, M, N, K,
+                                 _lib.EPI_RESIDUAL), dev.ctx)
+torch.cuda.synchronize()
+for i in range(3):
+    y.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(y, ref), f"replay {i}"
+print("replays equal sys1hip_linear_bf16", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_in_a_fresh_process():
+    """A process whose very first call of the entry point is inside a graph
+    capture (set-up then runs under capture: symbol address and occupancy
+    queries, no counter-clearing kernel, counters zero from the module
+    load).  Run in a child process so that no earlier call did the set-up;
+    its replays must equal sys1hip_linear_bf16."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("[gpu] noalloc first call under capture (child process)", flush=True)
+    out = subprocess.run([sys.executable, "-c", _FIRST_CALL_UNDER_CAPTURE, root], capture_output=True,
+                         text=True, timeout=100)
+    print(out.stdout[-2000:], out.stderr[-2000:], flush=True)
+    assert out.returncode == 0
+    assert "replays equal" in out.stdout
