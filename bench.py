@@ -66,6 +66,9 @@ def parse():
                          "layout packed at load (contiguous 4 KB per 32 rows and k-step; "
                          "sys1hip_pack_blocked_weight), which the default uses: same results bit for bit, "
                          "measured 0-5%% faster, most at small M")
+    ap.add_argument("--chain", choices=("on", "off"), default="off",
+                    help="on: each row-local run of projections (between two attention calls) is one "
+                         "persistent launch (sys1hip_linear_chain_bf16)")
     ap.add_argument("--graph", action="store_true",
                     help="replay one HIP graph per prepared batch instead of enqueueing every "
                          "projection from the host (measured: no difference on one MI355X)")
@@ -364,7 +367,7 @@ def main():
         from sys1_amd import kernel_names
         dev.set_kernel(kernel_names().index(args.kernel))
     stack = ProjectionStack(cfg, dev, max_m, seed=args.seed, norms=args.norms, conv=args.conv,
-                            blocked=not args.row_major)
+                            blocked=not args.row_major, chain=args.chain == "on")
     gen = torch.Generator(device="cuda:0")
     gen.manual_seed(args.seed + 1000)
     x = torch.randn(max_m, cfg.hidden, generator=gen, device="cuda:0").to(torch.bfloat16)
@@ -532,6 +535,8 @@ def main():
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) random-init weights)",
         "config": {"workload": f"{cfg.name} projection stack: {cfg.description}; {batch_desc}",
                    "launch": "one HIP graph per prepared batch" if args.graph else "eager",
+                   "chains": "one launch per row-local run of projections" if args.chain == "on"
+                   else "one launch per projection",
                    **({"forced_kernel": args.kernel} if args.kernel else {}),
                    "pre_norms": "fused (row statistics + folded norm weights)" if args.norms
                    else "none (projections only)",

@@ -112,6 +112,59 @@ SYS1HIP_API int sys1hip_linear_bf16(void* ctx,
                         int64_t M, int64_t N, int64_t K,
                         int32_t epilogue);
 
+/* One projection of a chain (sys1hip_linear_chain_bf16): the arguments of
+ * sys1hip_linear_bf16 for it, without bias. */
+typedef struct sys1hip_chain_proj {
+  const uint16_t* x; int64_t ldx;          /* [M,K] bf16 */
+  const uint16_t* w; int64_t ldw;          /* [N,K] bf16, or blocked (SYS1HIP_EPI_BLOCKED_W) */
+  const uint16_t* residual; int64_t ldr;   /* [M,Nout], required iff SYS1HIP_EPI_RESIDUAL */
+  uint16_t* y; int64_t ldy;                /* [M,Nout] */
+  int64_t N, K;
+  int32_t epilogue;                        /* NONE, RESIDUAL, GEGLU or SWIGLU (| BLOCKED_W) */
+} sys1hip_chain_proj;
+
+/* `count` (1..4) consecutive projections of one layer in one launch: the
+ * row-local run of a layer between two attention calls, e.g. ModernBERT's
+ * attn.Wo(+residual) -> Wi(+GeGLU) -> mlp.Wo(+residual) -> next layer's Wqkv
+ * (src/archs/modernbert.rs:857-887: the `.apply(&linear)` calls at :191,
+ * :522, :525-532 and the next layer's :184-187), or Qwen3.5's out_proj ->
+ * gate_up(+SwiGLU) -> down(+residual) -> next in_proj
+ * (src/archs/qwen35_text.rs:932-940).  Same results, bit for bit, as the
+ * same projections issued one sys1hip_linear_bf16 call each.
+ * Contract: projection p may read (as x or residual) rows that projections
+ * before it wrote, at the same rows only -- a token row of p depends on
+ * nothing but that row of earlier projections (attention, which mixes rows,
+ * must not sit inside a chain).  Projection p's rows are computed after
+ * projection p-1 has finished those rows.
+ * K must be a multiple of 64 and at least 192; gated epilogues need N % 32 ==
+ * 0; a residual needs Nout and ldr multiples of 8.  M <= 131072.
+ * One persistent launch on the context's stream; a dependency wait that
+ * does not resolve within the context's limit (sys1hip_set_chain_wait) is
+ * abandoned and flagged instead of hanging: check sys1hip_chain_status. */
+SYS1HIP_API int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t count, int64_t M);
+
+/* The chain kernel's tile queue of XCD `xcc` (no device needed; for
+ * host-side tests of the schedule, no counterpart in the reference): for
+ * `count` projections of N[p] output rows over M tokens, writes (projection,
+ * row panel, column tile) of each queue entry, in queue order, into
+ * tiles[3 i .. 3 i + 2] (up to `cap` ints) and returns the queue length. */
+SYS1HIP_API int sys1hip_chain_queue(int32_t xcc, int64_t M, int32_t count, const int64_t* N, int32_t* tiles,
+                        int64_t cap);
+
+/* Synchronise the context's stream and return (in *flags) the error bits
+ * that chain launches since the last call set, then clear them: 1 = a
+ * dependency wait expired (the results of that launch are not valid),
+ * 2 = a row panel's queue was not drained, 4 = a workgroup ran on an
+ * unexpected XCD id.  0 means every chain launch completed normally. */
+SYS1HIP_API int sys1hip_chain_status(void* ctx, int32_t* flags);
+
+/* Test and tuning knob, no counterpart in the reference: the real time (in
+ * microseconds, 1..10^6, default 20000) a chain dependency wait may take
+ * before it gives up, and an amount added to every dependency target (> 0
+ * makes every wait expire: the error path, exercised without a hang).  Once
+ * one wait of a launch has expired, its other waits give up at once. */
+SYS1HIP_API int sys1hip_set_chain_wait(void* ctx, int32_t wait_us, int32_t extra);
+
 /* Re-order a gated weight [2I, K] = [gate rows; up rows] (the reference's
  * chunk(2) split, src/archs/modernbert.rs:531-532, or gate_proj/up_proj
  * stacked, src/archs/qwen35_text.rs:205-231) into groups of 16 gate rows

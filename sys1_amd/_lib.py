@@ -40,8 +40,22 @@ EXPORTS = (
     "sys1hip_set_dp_tiles", "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
     "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_linear_bf16_noalloc",
     "sys1hip_blocked_weight_bytes", "sys1hip_pack_blocked_weight", "sys1hip_plan_kernel",
-    "sys1hip_plan_kernel_strided",
+    "sys1hip_plan_kernel_strided", "sys1hip_linear_chain_bf16", "sys1hip_chain_status",
+    "sys1hip_set_chain_wait", "sys1hip_chain_queue",
 )
+
+
+class ChainProj(ctypes.Structure):
+    """sys1hip_chain_proj: one projection of a chain launch."""
+    _fields_ = [("x", ctypes.c_void_p), ("ldx", ctypes.c_int64),
+                ("w", ctypes.c_void_p), ("ldw", ctypes.c_int64),
+                ("residual", ctypes.c_void_p), ("ldr", ctypes.c_int64),
+                ("y", ctypes.c_void_p), ("ldy", ctypes.c_int64),
+                ("N", ctypes.c_int64), ("K", ctypes.c_int64),
+                ("epilogue", ctypes.c_int32)]
+
+
+CHAIN_MAX = 4  # projections per chain launch
 
 
 class Sys1HipError(RuntimeError):
@@ -93,6 +107,10 @@ def load() -> ctypes.CDLL:
                                            i64, i64, i64, i32]
     L.sys1hip_linear_conv_silu_bf16.argtypes = [vp, vp, i64, vp, i64, i32, ctypes.c_float, vp, i64, vp,
                                                 vp, i64, i64, i64, i64]
+    L.sys1hip_linear_chain_bf16.argtypes = [vp, ctypes.POINTER(ChainProj), i32, i64]
+    L.sys1hip_chain_status.argtypes = [vp, ctypes.POINTER(i32)]
+    L.sys1hip_set_chain_wait.argtypes = [vp, i32, i32]
+    L.sys1hip_chain_queue.argtypes = [i32, i64, i32, ctypes.POINTER(i64), ctypes.POINTER(i32), i64]
     L.sys1hip_kernel_count.argtypes = []
     L.sys1hip_kernel_name.argtypes = [i32]
     L.sys1hip_kernel_name.restype = ctypes.c_char_p
@@ -102,7 +120,8 @@ def load() -> ctypes.CDLL:
                  "sys1hip_linear_rope_qkv_bf16", "sys1hip_fold_norm_weight",
                  "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_kernel_count",
                  "sys1hip_linear_bf16_noalloc", "sys1hip_pack_blocked_weight", "sys1hip_plan_kernel",
-                 "sys1hip_plan_kernel_strided"):
+                 "sys1hip_plan_kernel_strided", "sys1hip_linear_chain_bf16", "sys1hip_chain_status",
+                 "sys1hip_set_chain_wait", "sys1hip_chain_queue"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L
@@ -126,6 +145,17 @@ def plan_kernel(M: int, N: int, K: int, epilogue: int = 0, cus: int = 256,
     kid = check(L.sys1hip_plan_kernel_strided(cus, M, N, K, ldx or K, ldw or K, epilogue,
                                               ctypes.byref(grid), buf, 96))
     return kid, grid.value, buf.value.decode()
+
+
+def chain_queue(xcc: int, M: int, Ns: list[int]) -> list[tuple[int, int, int]]:
+    """The chain kernel's tile queue of one XCD: (projection, row panel,
+    column tile) in the order its workgroups take them."""
+    L = load()
+    n_arr = (ctypes.c_int64 * len(Ns))(*Ns)
+    total = check(L.sys1hip_chain_queue(xcc, M, len(Ns), n_arr, None, 0))
+    buf = (ctypes.c_int32 * (3 * total))()
+    check(L.sys1hip_chain_queue(xcc, M, len(Ns), n_arr, buf, 3 * total))
+    return [(buf[3 * i], buf[3 * i + 1], buf[3 * i + 2]) for i in range(total)]
 
 
 def kernel_names() -> list[str]:

@@ -18,6 +18,7 @@
 #include "kernel_fns.hpp"
 #include "norm.hpp"
 #include "conv.hpp"
+#include "chain.hpp"
 
 using namespace sys1;
 
@@ -83,6 +84,12 @@ struct Context {
   float* ws = nullptr;
   unsigned* counters = nullptr;
   float* stats = nullptr;  // pre-norm row statistics, kNormRows x (mean, 1/std)
+  // Projection chains: the dependency bank (zero between launches: each
+  // launch's last workgroup clears it) and the error word, one allocation.
+  unsigned* chain = nullptr;
+  int chain_wait_us = 20000;  // real time a dependency wait may take before it gives up
+  int chain_extra = 0;
+  int chain_occ = 0;         // resident chain workgroups per CU
   int forced_kernel = -1;
   int forced_grid = 0;
   int forced_dp = -1;
@@ -597,9 +604,12 @@ int sys1hip_init(int device, void** out) {
       hipMalloc(&c->ws, kWorkspaceBytes) != hipSuccess ||
       hipMalloc(&c->counters, kCounterSlots * sizeof(unsigned)) != hipSuccess ||
       hipMalloc(&c->stats, kNormRows * 2 * sizeof(float)) != hipSuccess ||
+      hipMalloc(&c->chain, (kChainBankWords + 64) * sizeof(unsigned)) != hipSuccess ||
       hipMemsetAsync(c->counters, 0, kCounterSlots * sizeof(unsigned), c->own) != hipSuccess ||
+      hipMemsetAsync(c->chain, 0, (kChainBankWords + 64) * sizeof(unsigned), c->own) != hipSuccess ||
       hipStreamSynchronize(c->own) != hipSuccess) {
     const char* msg = hipGetErrorString(hipGetLastError());
+    if (c->chain) (void)hipFree(c->chain);
     if (c->stats) (void)hipFree(c->stats);
     if (c->counters) (void)hipFree(c->counters);
     if (c->ws) (void)hipFree(c->ws);
@@ -618,6 +628,9 @@ int sys1hip_init(int device, void** out) {
                                                              kKernels[id].threads, 0) == hipSuccess)
         c->occ[(size_t)id * kEpiCount + epi] = n;
     }
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&c->chain_occ, kChainKernel.fn, kChainKernel.threads, 0) !=
+      hipSuccess)
+    c->chain_occ = 0;
   (void)hipGetLastError();
   *out = c;
   return SYS1HIP_OK;
@@ -629,6 +642,7 @@ int sys1hip_destroy(void* ctx) {
   int rc = use_device(c);
   if (rc) return rc;
   HIP_TRY(hipStreamSynchronize(c->stream));
+  (void)hipFree(c->chain);
   (void)hipFree(c->stats);
   (void)hipFree(c->counters);
   (void)hipFree(c->ws);
@@ -1172,6 +1186,112 @@ int sys1hip_pack_gated_weight(void* ctx, const uint16_t* w, uint16_t* packed, in
   hipLaunchKernelGGL(pack_gated_kernel, dim3((unsigned)blocks), dim3(256), 0, c->stream,
                      reinterpret_cast<const i32x4*>(w), reinterpret_cast<i32x4*>(packed), N, kv);
   HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+
+// ---- projection chains (chain.hip)
+
+int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t count, int64_t M) {
+  static const char* who = "sys1hip_linear_chain_bf16";
+  if (!ctx) return fail(SYS1HIP_EINVAL, "%s: null context", who);
+  if (!proj || count < 1 || count > kChainMax)
+    return fail(SYS1HIP_EINVAL, "%s: %d projections (1..%d)", who, (int)count, kChainMax);
+  if (M < 0) return fail(SYS1HIP_EINVAL, "%s: M=%lld", who, (long long)M);
+  Context* c = static_cast<Context*>(ctx);
+  const ChainKernel& ck = kChainKernel;
+  const int64_t panels = cdiv(M, ck.bm);
+  if (panels > kChainMaxPanels)
+    return fail(SYS1HIP_ERANGE, "%s: M=%lld above %lld tokens", who, (long long)M, (long long)kChainMaxPanels * ck.bm);
+  ChainArgs a{};
+  for (int p = 0; p < count; ++p) {
+    const sys1hip_chain_proj& q = proj[p];
+    int rc = check_linear(who, q.x, q.ldx, q.w, q.ldw, nullptr, q.residual, q.ldr, q.y, q.ldy, M, q.N, q.K,
+                          q.epilogue);
+    if (rc) return rc;
+    const int epi = epi_id_from_flags(q.epilogue);
+    if (epi != kEpiNone && epi != kEpiResidual && epi != kEpiGeglu && epi != kEpiSwiglu)
+      return fail(SYS1HIP_EINVAL, "%s: projection %d: epilogue flags %d (none, residual, GeGLU or SwiGLU)", who, p,
+                  q.epilogue);
+    if (q.K % kBlkK || q.K / kBlkK < ck.stages)
+      return fail(SYS1HIP_EINVAL, "%s: projection %d: K=%lld must be a multiple of %d and at least %d", who, p,
+                  (long long)q.K, kBlkK, kBlkK * ck.stages);
+    const int64_t nout = epi_gated(epi) ? q.N / 2 : q.N;
+    if (epi == kEpiResidual &&
+        (nout % 8 || q.ldr % 8 || !aligned16(q.residual) || 2 * (M * q.ldr + nout) >= 0x7ffffff0ll))
+      return fail(SYS1HIP_EALIGN, "%s: projection %d: the residual needs Nout and ldr multiples of 8, 16-byte "
+                  "alignment and fewer than 2 GiB of rows", who, p);
+    if (2 * (int64_t)ck.bm * q.ldx + 2 * q.K >= 0x7ffffff0ll || (!(q.epilogue & SYS1HIP_EPI_BLOCKED_W) &&
+                                                                2 * (int64_t)ck.bn * q.ldw >= 0x7ffffff0ll))
+      return fail(SYS1HIP_ERANGE, "%s: projection %d: leading dimension too large", who, p);
+    ChainProj& P = a.proj[p];
+    P.x = reinterpret_cast<const __bf16*>(q.x);
+    P.w = reinterpret_cast<const __bf16*>(q.w);
+    P.resid = reinterpret_cast<const __bf16*>(q.residual);
+    P.y = reinterpret_cast<__bf16*>(q.y);
+    P.ldx = q.ldx, P.ldw = q.ldw, P.ldr = q.ldr, P.ldy = q.ldy;
+    P.N = (int)q.N, P.K = (int)q.K, P.Nout = (int)nout, P.epi = epi;
+    P.w_kt = (q.epilogue & SYS1HIP_EPI_BLOCKED_W) ? (int)cdiv(q.K, kBlkK) : 0;
+    P.tiles_n = (int)cdiv(q.N, ck.bn);
+    P.kt_count = (int)(q.K / kBlkK);
+  }
+  if (M == 0) return SYS1HIP_OK;
+  int rc = use_device(c);
+  if (rc) return rc;
+  if (c->chain_occ < 1) return fail(SYS1HIP_EDEVICE, "%s: the chain kernel cannot be resident on this device", who);
+  a.bank = c->chain;
+  a.err = c->chain + kChainBankWords;
+  a.nproj = count;
+  a.M = (int)M;
+  a.row_panels = (int)panels;
+  a.nxcd = kChainXcdMax;
+  a.wait_us = c->chain_wait_us;
+  a.dep_extra = c->chain_extra;
+  const int grid = c->cus * c->chain_occ;
+  hipLaunchKernelGGL(reinterpret_cast<void (*)(ChainArgs)>(const_cast<void*>(ck.fn)), dim3((unsigned)grid),
+                     dim3(ck.threads), 0, c->stream, a);
+  HIP_TRY(hipGetLastError());
+  return SYS1HIP_OK;
+}
+
+int sys1hip_chain_queue(int32_t xcc, int64_t M, int32_t count, const int64_t* N, int32_t* tiles, int64_t cap) {
+  if (count < 1 || count > kChainMax || !N || xcc < 0 || xcc >= kChainXcdMax || M < 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_chain_queue: bad arguments");
+  const int64_t panels = cdiv(M, kChainKernel.bm);
+  if (panels > kChainMaxPanels) return fail(SYS1HIP_ERANGE, "sys1hip_chain_queue: M=%lld", (long long)M);
+  int tn[kChainMax] = {};
+  for (int p = 0; p < count; ++p) {
+    if (N[p] <= 0) return fail(SYS1HIP_EINVAL, "sys1hip_chain_queue: N[%d]=%lld", p, (long long)N[p]);
+    tn[p] = (int)cdiv(N[p], kChainKernel.bn);
+  }
+  const XcdQueue q(xcc, kChainXcdMax, (int)panels, count, tn);
+  for (int i = 0; i < q.total && tiles && 3 * (int64_t)i + 2 < cap; ++i) {
+    const ChainTile t = q.decode(i);
+    tiles[3 * i] = t.p, tiles[3 * i + 1] = t.rp, tiles[3 * i + 2] = t.tn;
+  }
+  return q.total;
+}
+
+int sys1hip_chain_status(void* ctx, int32_t* flags) {
+  if (!ctx || !flags) return fail(SYS1HIP_EINVAL, "sys1hip_chain_status: null argument");
+  Context* c = static_cast<Context*>(ctx);
+  int rc = use_device(c);
+  if (rc) return rc;
+  unsigned v = 0;
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  HIP_TRY(hipMemcpy(&v, c->chain + kChainBankWords, sizeof(v), hipMemcpyDeviceToHost));
+  if (v) HIP_TRY(hipMemset(c->chain + kChainBankWords, 0, sizeof(v)));
+  *flags = (int32_t)v;
+  return SYS1HIP_OK;
+}
+
+int sys1hip_set_chain_wait(void* ctx, int32_t wait_us, int32_t extra) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_set_chain_wait: null context");
+  if (wait_us < 1 || wait_us > 1000000 || extra < 0)
+    return fail(SYS1HIP_EINVAL, "sys1hip_set_chain_wait: wait_us %d (1..1000000), extra %d", (int)wait_us,
+                (int)extra);
+  Context* c = static_cast<Context*>(ctx);
+  c->chain_wait_us = wait_us;
+  c->chain_extra = extra;
   return SYS1HIP_OK;
 }
 

@@ -50,6 +50,19 @@ class HipDevice:
         phase (-1 = automatic)."""
         _lib.check(self._L.sys1hip_set_dp_tiles(self.ctx, int(tiles)), self.ctx)
 
+    def chain_status(self) -> int:
+        """Synchronise and return (then clear) the error bits of the chain
+        launches since the last call (sys1hip_chain_status); 0 = all fine."""
+        v = ctypes.c_int32()
+        _lib.check(self._L.sys1hip_chain_status(self.ctx, ctypes.byref(v)), self.ctx)
+        return v.value
+
+    def set_chain_wait(self, wait_us: int = 20000, extra: int = 0) -> None:
+        """Real time a chain dependency wait may take before it gives up, and
+        an amount added to every dependency target (a test knob: > 0 makes
+        every wait expire)."""
+        _lib.check(self._L.sys1hip_set_chain_wait(self.ctx, int(wait_us), int(extra)), self.ctx)
+
     def query_kernel(self, M: int, N: int, K: int, epilogue: int = 0) -> tuple[int, str]:
         buf = ctypes.create_string_buffer(96)
         kid = _lib.check(self._L.sys1hip_query_kernel(self.ctx, M, N, K, epilogue, buf, 96), self.ctx)

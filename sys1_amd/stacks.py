@@ -44,6 +44,7 @@ class Proj:
     resid: str | None = None
     norm: str | None = None  # pre-norm of the input ("layer" / "rms"), fused when the stack has norms
     conv_ch: int = 0         # leading output columns under the DeltaNet causal conv + SiLU
+    mixes_rows: bool = False  # its input comes from a row-mixing op (attention, the DeltaNet recurrence)
 
     @property
     def nout(self) -> int:
@@ -84,7 +85,7 @@ def modernbert(hidden: int, intermediate: int, layers: int, name: str) -> StackC
     def layer(i: int) -> list[Proj]:
         return [
             Proj("Wqkv", H, 3 * H, _lib.EPI_NONE, "h", 0, "qkv", norm="layer" if i > 0 else None),
-            Proj("attn.Wo", H, H, _lib.EPI_RESIDUAL, "qkv", 2 * H, "h", resid="h"),
+            Proj("attn.Wo", H, H, _lib.EPI_RESIDUAL, "qkv", 2 * H, "h", resid="h", mixes_rows=True),
             Proj("Wi+geglu", H, 2 * I, _lib.EPI_GEGLU, "h", 0, "act", norm="layer"),
             Proj("mlp.Wo", I, H, _lib.EPI_RESIDUAL, "act", 0, "h", resid="h"),
         ]
@@ -111,13 +112,13 @@ def qwen35(hidden: int, layers: int, heads: int, kv_heads: int, head_dim: int,
     deltanet = [
         Proj("in_proj_qkvzba", H, dn_in, _lib.EPI_NONE, "h", 0, "mix", norm="rms",
              conv_ch=2 * dn_qk + dn_v),
-        Proj("out_proj", dn_v, H, _lib.EPI_RESIDUAL, "mix", 2 * dn_qk + dn_v, "h", resid="h"),
+        Proj("out_proj", dn_v, H, _lib.EPI_RESIDUAL, "mix", 2 * dn_qk + dn_v, "h", resid="h", mixes_rows=True),
     ] + mlp
     q_w = 2 * heads * head_dim
     attn_in = q_w + 2 * kv_heads * head_dim
     attention = [
         Proj("q_k_v", H, attn_in, _lib.EPI_NONE, "h", 0, "mix", norm="rms"),
-        Proj("o_proj", o_in, H, _lib.EPI_RESIDUAL, "mix", 0, "h", resid="h"),
+        Proj("o_proj", o_in, H, _lib.EPI_RESIDUAL, "mix", 0, "h", resid="h", mixes_rows=True),
     ] + mlp
     if layer_types is None:
         layer_types = ["full_attention" if (i + 1) % 4 == 0 else "linear_attention" for i in range(layers)]
@@ -157,6 +158,13 @@ class ProjectionStack:
     (Proj.conv_ch columns; conv weights N(0, 0.5^2) or `conv_weights`
     [layer] -> [conv_ch, 4]); the calls then need per-token positions.
 
+    chain=True runs each row-local run of projections (from one row-mixing
+    op to the next: attention, the DeltaNet recurrence) as one launch
+    (sys1hip_linear_chain_bf16, at most 4 projections each), bit for bit the
+    results of the per-projection calls; it applies to stacks without fused
+    norms or conv, and projections the chain kernel does not take (K not a
+    multiple of 64 or below 192) run as single calls.
+
     blocked=True stores the weights in the blocked layout
     (linear.pack_blocked_weight: contiguous 4 KB per 32 rows and k-step,
     what the weight-streaming kernels read best), after any gate/up packing
@@ -167,7 +175,8 @@ class ProjectionStack:
                  weights: list[list[torch.Tensor]] | None = None, w_std: float = 0.02,
                  norms: bool = False, norm_weights: list[list[torch.Tensor | None]] | None = None,
                  norm_eps: dict[str, float] | None = None, conv: bool = False,
-                 conv_weights: list[torch.Tensor | None] | None = None, blocked: bool = False):
+                 conv_weights: list[torch.Tensor | None] | None = None, blocked: bool = False,
+                 chain: bool = False):
         self.cfg = cfg
         self.dev = dev
         self.max_tokens = max_tokens
@@ -178,6 +187,9 @@ class ProjectionStack:
         from .norm import fold_norm_weight
         self.norms = norms
         self.blocked = blocked
+        if chain and (norms or conv):
+            raise ValueError("chain=True runs projections without fused norms or conv")
+        self.chain = chain
         self.conv = conv
         self.conv_w: list[torch.Tensor | None] = []
         self.norm_eps = dict(NORM_EPS, **(norm_eps or {}))
@@ -223,6 +235,7 @@ class ProjectionStack:
         self._fn = dev._L.sys1hip_linear_bf16
         self._norm_fn = dev._L.sys1hip_norm_linear_bf16
         self._conv_fn = dev._L.sys1hip_linear_conv_silu_bf16
+        self._chain_fn = dev._L.sys1hip_linear_chain_bf16
 
     def _calls(self, x: torch.Tensor, M: int, positions: torch.Tensor | None = None) -> list[tuple]:
         """Argument tuples of every launch for M tokens (prepared once per M,
@@ -274,11 +287,51 @@ class ProjectionStack:
                                                 p.epi | (_lib.EPI_BLOCKED_W if self.blocked else 0))))
         return calls
 
+    @staticmethod
+    def _chainable(p: Proj) -> bool:
+        return p.K % 64 == 0 and p.K >= 192 and p.epi in (
+            _lib.EPI_NONE, _lib.EPI_RESIDUAL, _lib.EPI_GEGLU, _lib.EPI_SWIGLU)
+
+    def _chain_calls(self, calls: list[tuple], M: int) -> list[tuple]:
+        """Group the per-projection calls into chain launches: a run ends
+        before a projection whose input is row-mixed, after CHAIN_MAX
+        projections, and around a projection the chain kernel does not take
+        (that one stays a single call)."""
+        out, run = [], []
+
+        def flush():
+            if not run:
+                return
+            arr = (_lib.ChainProj * len(run))()
+            for i, (p, _, a) in enumerate(run):
+                src, ldx, w, ldw, _bias, rptr, ldr, dst, ldy, _M, N, K, epi = a
+                arr[i] = _lib.ChainProj(src, ldx, w, ldw, rptr, ldr, dst, ldy, N, K, epi)
+            out.append((tuple(p for p, _, _ in run), self._chain_fn, (self.dev.ctx, arr, len(run), M)))
+            run.clear()
+
+        for p, fn, a in calls:
+            if fn is not self._fn or not self._chainable(p):
+                flush()
+                out.append((p, fn, a))
+                continue
+            if p.mixes_rows or len(run) == _lib.CHAIN_MAX:
+                flush()
+            run.append((p, fn, a))
+        flush()
+        return out
+
     def prepare(self, x: torch.Tensor, M: int, positions: torch.Tensor | None = None):
-        """[(projection, C function, argument tuple)] of every launch."""
+        """[(projection, C function, argument tuple)] of every launch (a chain
+        launch carries the tuple of its projections)."""
         ctx = self.dev.ctx
         out = []
-        for p, fn, args in self._calls(x, M, positions):
+        calls = self._calls(x, M, positions)
+        if self.chain:
+            calls = self._chain_calls(calls, M)
+        for p, fn, args in calls:
+            if fn is self._chain_fn:
+                out.append((p, fn, args))
+                continue
             ptrs = ((0, 2, 4, 7) if fn is self._norm_fn else (0, 2, 6, 8, 9) if fn is self._conv_fn
                     else (0, 2, 4, 5, 7))
             out.append((p, fn, (ctx, *[ctypes.c_void_p(a) if i in ptrs and a is not None else a
