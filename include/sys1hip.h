@@ -165,6 +165,13 @@ SYS1HIP_API int sys1hip_chain_status(void* ctx, int32_t* flags);
  * one wait of a launch has expired, its other waits give up at once. */
 SYS1HIP_API int sys1hip_set_chain_wait(void* ctx, int32_t wait_us, int32_t extra);
 
+/* Measurement knob, no counterpart in the reference: a device buffer that
+ * later chain launches fill with their timeline (null: off), 64 records of
+ * 4 x u64 per workgroup -- {queue index | XCD << 32 | drained << 40, start,
+ * stores done, projection}, on the 100 MHz constant clock; it must hold
+ * workgroups x 64 x 32 bytes (CUs workgroups), else nothing is recorded. */
+SYS1HIP_API int sys1hip_set_chain_trace(void* ctx, void* buffer, int64_t bytes);
+
 /* Re-order a gated weight [2I, K] = [gate rows; up rows] (the reference's
  * chunk(2) split, src/archs/modernbert.rs:531-532, or gate_proj/up_proj
  * stacked, src/archs/qwen35_text.rs:205-231) into groups of 16 gate rows

@@ -41,7 +41,7 @@ EXPORTS = (
     "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_linear_bf16_noalloc",
     "sys1hip_blocked_weight_bytes", "sys1hip_pack_blocked_weight", "sys1hip_plan_kernel",
     "sys1hip_plan_kernel_strided", "sys1hip_linear_chain_bf16", "sys1hip_chain_status",
-    "sys1hip_set_chain_wait", "sys1hip_chain_queue",
+    "sys1hip_set_chain_wait", "sys1hip_chain_queue", "sys1hip_set_chain_trace",
 )
 
 
@@ -110,6 +110,7 @@ def load() -> ctypes.CDLL:
     L.sys1hip_linear_chain_bf16.argtypes = [vp, ctypes.POINTER(ChainProj), i32, i64]
     L.sys1hip_chain_status.argtypes = [vp, ctypes.POINTER(i32)]
     L.sys1hip_set_chain_wait.argtypes = [vp, i32, i32]
+    L.sys1hip_set_chain_trace.argtypes = [vp, vp, i64]
     L.sys1hip_chain_queue.argtypes = [i32, i64, i32, ctypes.POINTER(i64), ctypes.POINTER(i32), i64]
     L.sys1hip_kernel_count.argtypes = []
     L.sys1hip_kernel_name.argtypes = [i32]
@@ -121,7 +122,7 @@ def load() -> ctypes.CDLL:
                  "sys1hip_norm_linear_bf16", "sys1hip_linear_conv_silu_bf16", "sys1hip_kernel_count",
                  "sys1hip_linear_bf16_noalloc", "sys1hip_pack_blocked_weight", "sys1hip_plan_kernel",
                  "sys1hip_plan_kernel_strided", "sys1hip_linear_chain_bf16", "sys1hip_chain_status",
-                 "sys1hip_set_chain_wait", "sys1hip_chain_queue"):
+                 "sys1hip_set_chain_wait", "sys1hip_chain_queue", "sys1hip_set_chain_trace"):
         getattr(L, name).restype = ctypes.c_int
     _lib = L
     return L

@@ -54,6 +54,12 @@ namespace sys1 {
 namespace {
 
 constexpr int kPolicySc0 = 1;  // buffer cache policy: sc0 (miss in the CU's L1, read the L2)
+#ifndef SYS1_X_POLICY
+#define SYS1_X_POLICY kPolicySc0
+#endif
+#ifndef SYS1_RES_POLICY
+#define SYS1_RES_POLICY kPolicySc0
+#endif
 
 __device__ __forceinline__ int hw_xcc_id() {
   int v;
@@ -113,6 +119,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
   __shared__ __attribute__((aligned(1024))) char lds[S::kLdsBytes];
   __shared__ int slot_id[4];     // queue index of tile n (n % 4), -1 past the end
   __shared__ int slot_ready[4];  // its dependency was met when it was taken
+  __shared__ int drain_met;      // tile sequence number whose deferred dependency producer 0 saw met
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -137,21 +144,25 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
   // Bounded wait for a tile's dependency: at most wait_us of real time (the
   // 100 MHz constant clock), and none at all once any wait of this launch
   // has expired.  An expired wait is reported and passed: the launch still
-  // finishes, and its results are then not to be used.
+  // finishes, and its results are then not to be used.  One wave per
+  // workgroup polls, backing off to about a microsecond between polls: the
+  // counters of a row panel are polled by every workgroup that waits for
+  // it, and faster polling floods the memory channel that holds them.
   auto wait_dep = [&](const ChainTile& t) {
     if (dep_met(t)) return;
     if (atomic_load_agent(aborted)) return;
     const uint64_t t0 = wall_clock64();
     const uint64_t budget = (uint64_t)a->wait_us * 100;
     for (int n = 1; !dep_met(t); ++n) {
-      if (wall_clock64() - t0 > budget || ((n & 63) == 0 && atomic_load_agent(aborted))) {
+      if (wall_clock64() - t0 > budget || ((n & 15) == 0 && atomic_load_agent(aborted))) {
         if (lane == 0) {
           __hip_atomic_store(aborted, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_fetch_or(a->err, kChainErrTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
       }
-      __builtin_amdgcn_s_sleep(2);
+      if (n < 4) __builtin_amdgcn_s_sleep(8);
+      else __builtin_amdgcn_s_sleep(32);
     }
   };
   // Compute wave 0 takes the tiles: the next one is taken (one atomic) when
@@ -176,6 +187,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
     }
   };
   const bool producer = wave >= kWaves;
+  if (tid == 0) drain_met = 0;
   if (active && wave == 0) {
     const int id = id_of(grab());
     if (id >= 0) wait_dep(q.decode(id));
@@ -227,7 +239,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
       for (int i = 0; i < kDma; ++i) {
         lds_void* dst = (lds_void*)(base + (i * kDW + dwave) * 1024);
         if (i < kXDma)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst, 16, (int)src_off[i], xk, 0, kPolicySc0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst, 16, (int)src_off[i], xk, 0, SYS1_X_POLICY);
         else
           __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, dst, 16, (int)src_off[i], wk, 0, 0);
       }
@@ -263,7 +275,13 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
       if (s == last_step) break;
       if (s == drain_at) {
         const ChainTile nt = q.decode(next_id);
-        wait_dep(nt);
+        if (dwave == 0) {
+          wait_dep(nt);
+          if (lane == 0) __hip_atomic_store(&drain_met, n + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else {
+          while (__hip_atomic_load(&drain_met, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) != n + 1)
+            __builtin_amdgcn_s_sleep(2);
+        }
         ++n;
         it = nt;
         w_kt_cur = CHAIN_FIELD(a, it.p, w_kt);
@@ -349,7 +367,35 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
       const int m0 = t.rp * BM, n0 = t.tn * BN;
       constexpr bool kGated = E == kEpiGeglu || E == kEpiSwiglu;
       const int out_n0 = kGated ? (n0 + wn * S::TN) / 2 : n0 + wn * S::TN;
-      const rsrc_t rr = make_rsrc_uniform(E == kEpiResidual ? P.resid : P.y, 0x7ffffff0);
+      // The residual of every element this lane stores is loaded first, all
+      // loads in flight together: y may alias the residual (the in-place
+      // update of the hidden state), so a load issued after a store could
+      // not be moved ahead of it, and each would wait a full round trip.
+      // Each lane reads exactly the elements it then writes, so reading all
+      // of them first is correct for an in-place update too.
+      bf16x8 res[S::FM][S::FN][2];
+      if constexpr (E == kEpiResidual) {
+        const rsrc_t rr = make_rsrc_uniform(P.resid, 0x7ffffff0);
+#pragma unroll
+        for (int j = 0; j < S::FM; ++j) {
+          const int m = m0 + wm * S::TM + j * 32 + frow;
+#pragma unroll
+          for (int i = 0; i < S::FN; ++i)
+#pragma unroll
+            for (int gp = 0; gp < 2; ++gp) {
+              const int nn = out_n0 + i * 32 + 16 * gp + 8 * fk;
+              // (Nout % 8 == 0, 16-byte aligned rows, M ldr 2 < 2 GiB: checked
+              // by the host; rows past M and columns past Nout read zeros)
+              const unsigned off = m < a->M && nn < P.Nout ? (unsigned)(((int64_t)m * P.ldr + nn) * 2) : kOutOfRange;
+#ifdef SYS1_RES_NOLOAD
+              res[j][i][gp] = bf16x8{};
+              (void)off;
+#else
+              res[j][i][gp] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rr, (int)off, 0, SYS1_RES_POLICY));
+#endif
+            }
+        }
+      }
 #pragma unroll
       for (int j = 0; j < S::FM; ++j) {
         const int m = m0 + wm * S::TM + j * 32 + frow;
@@ -377,12 +423,8 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
               const int nn = out_n0 + i * 32 + 16 * gp + 8 * fk;
               if (row_ok && nn < P.Nout) {
                 if constexpr (E == kEpiResidual) {
-                  // (Nout % 8 == 0, 16-byte aligned rows, M ldr 2 < 2 GiB: checked by the host)
-                  const i32x4 rv = __builtin_amdgcn_raw_buffer_load_b128(
-                      rr, (int)(((int64_t)m * P.ldr + nn) * 2), 0, kPolicySc0);
-                  const bf16x8 r8 = __builtin_bit_cast(bf16x8, rv);
 #pragma unroll
-                  for (int e = 0; e < 8; ++e) v[e] = to_bf16(round_bf16(to_f32(v[e]) + to_f32(r8[e])));
+                  for (int e = 0; e < 8; ++e) v[e] = to_bf16(round_bf16(to_f32(v[e]) + to_f32(res[j][i][gp][e])));
                 }
                 store8(P.y + (int64_t)m * P.ldy + nn, v, P.Nout - nn);
               }
@@ -394,8 +436,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
     // Epilogue of tile t straight from registers (the layout and rounding of
     // gemm_tile_kernel's): lanes l and l+32 swap halves so every lane stores
     // 16 contiguous bytes; residual reads bypass the L1 (sc0), since another
-    // CU of this XCD may have written those rows during this launch.  Then
-    // this wave's part of the tile is counted, once its stores are done.
+    // CU of this XCD may have written those rows during this launch.
     auto epilogue = [&](const ChainTile& t) {
       using std::integral_constant;
       switch (CHAIN_FIELD(a, t.p, epi)) {
@@ -404,21 +445,43 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
         case kEpiSwiglu: epilogue_as(t, integral_constant<int, kEpiSwiglu>()); break;
         default: epilogue_as(t, integral_constant<int, kEpiNone>()); break;
       }
-      __builtin_amdgcn_s_waitcnt(0);
+    };
+    // This wave's part of tile t is counted once its stores are done.  When
+    // the next tile streams in, that happens a k-step into it (the MFMAs go
+    // on while the stores drain); before a drain or the end, at once (the
+    // next tile may depend on this one).
+    auto release = [&](const ChainTile& t) {
+      vm_wait<0>();
       if (lane == 0)
         __hip_atomic_fetch_add(deps + t.p * a->row_panels + t.rp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
+    bool pending = false;
+    ChainTile pend_tile{0, 0, 0};
 
     ChainTile ct = q.decode(first);
     int kc = CHAIN_FIELD(a, ct.p, kt_count);
     int ckt = 0;
     int n = 0;
+    int cur_id = first;
+    uint64_t t_start = 0, t_epi = 0;
+    bool drained = false;
+    unsigned long long* const trace = a->trace;
+    auto record = [&]() {
+      if (trace && wave == 0 && lane == 0 && n < kChainTraceTiles) {
+        unsigned long long* r = trace + ((size_t)blockIdx.x * kChainTraceTiles + n) * 4;
+        r[0] = (unsigned long long)cur_id | ((unsigned long long)q.xcc << 32) | ((unsigned long long)drained << 40);
+        r[1] = t_start;
+        r[2] = wall_clock64();
+        r[3] = (unsigned long long)ct.p | ((unsigned long long)(t_epi - t_start) << 8);
+      }
+    };
     zero_acc();
     Frags fr[4];
     unsigned next_raw = 0xffffffffu, poll_raw = 0;
     int next_id = -1;
     ChainTile next_tile{0, 0, 0};
     __syncthreads();  // B_start
+    if (trace) t_start = wall_clock64();
     read(fr[0], 0, 0);
     read(fr[1], 0, 1);
     int stage = 0;
@@ -433,8 +496,13 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
       __builtin_amdgcn_sched_barrier(0);
       mma(fr[1]);
       __builtin_amdgcn_sched_barrier(0);
+      const int rel_at = kc > STAGES + 1 ? 1 : 0;
+      if (pending && ckt == rel_at) {
+        release(pend_tile);
+        pending = false;
+      }
       if (wave == 0) {
-        if (ckt == 0) next_raw = grab();
+        if (ckt == rel_at) next_raw = grab();
         if (ckt == max(0, kc - STAGES - 1)) {
           next_id = id_of(next_raw);
           next_tile = next_id >= 0 ? q.decode(next_id) : ChainTile{0, 0, 0};
@@ -470,13 +538,26 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
         ++ckt;
         continue;
       }
+      if (trace) t_epi = wall_clock64();
       epilogue(ct);
       zero_acc();
+      if (streamed) {
+        pending = true;
+        pend_tile = ct;
+      } else {
+        release(ct);
+      }
+      if (trace) record();
       if (nid < 0) break;
       if (!streamed) {
         __syncthreads();  // barrier(D): the producers have the next tile's first k-tiles in
         read(fr[0], stage, 0);
         read(fr[1], stage, 1);
+      }
+      if (trace) {
+        t_start = wall_clock64();
+        drained = !streamed;
+        cur_id = nid;
       }
       ++n;
       ct = q.decode(nid);

@@ -38,7 +38,13 @@ struct ChainArgs {
   int nproj, M, row_panels, nxcd;
   int wait_us;          // real time a dependency wait may take before it gives up
   int dep_extra;        // added to every dependency target (test knob: forces the waits to expire)
+  // Optional timeline (null: off): per workgroup, kChainTraceTiles records of
+  // 4 x u64 {queue index | xcc << 32 | drained << 40, start, stores done,
+  // projection | (epilogue start - start) << 8}, times on the 100 MHz
+  // constant clock.
+  unsigned long long* trace;
 };
+constexpr int kChainTraceTiles = 64;
 
 // A tile of a queue: projection, row panel, column tile.
 struct ChainTile {

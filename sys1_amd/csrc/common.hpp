@@ -307,4 +307,12 @@ __device__ __forceinline__ void load8(const __bf16* p, float v[8], int valid) {
   }
 }
 
+// The same 8 values as bf16 (zeros past `valid`).
+__device__ __forceinline__ bf16x8 load8_bf16(const __bf16* p, int valid) {
+  if (valid >= 8 && aligned16(p)) return *reinterpret_cast<const bf16x8*>(p);
+  bf16x8 v;
+  for (int j = 0; j < 8; ++j) v[j] = j < valid ? p[j] : __bf16(0.0f);
+  return v;
+}
+
 }  // namespace sys1

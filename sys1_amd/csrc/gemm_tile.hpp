@@ -712,6 +712,29 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
     }
     const int h = fk;
     const int out_n0 = epi_gated(E) ? (n0 + wn * S::TN) / 2 : n0 + wn * S::TN;
+    // The residual of every element this lane stores, loaded before any
+    // store: y may alias it (the in-place update of the hidden state), and a
+    // load behind a store to a possibly aliasing address would wait a whole
+    // round trip each.  A lane reads exactly the elements it then writes, so
+    // reading them all first is correct in place too.
+    constexpr bool kResRegs = epi_has_resid<E>() && !epi_gated(E) && E != kEpiRopeQkv;
+    bf16x8 rres[kResRegs ? S::FM : 1][kResRegs ? S::FN : 1][2];
+    if constexpr (kResRegs) {
+      if (!(kResLds && res_in_lds)) {
+#pragma unroll
+        for (int j = 0; j < S::FM; ++j) {
+          const int m = m0 + wm * S::TM + j * 32 + frow;
+#pragma unroll
+          for (int i = 0; i < S::FN; ++i)
+#pragma unroll
+            for (int gp = 0; gp < 2; ++gp) {
+              const int n = out_n0 + i * 32 + 16 * gp + 8 * h;
+              rres[j][i][gp] = m < a.M && n < a.Nout ? load8_bf16(a.resid + (int64_t)m * a.ldr + n, a.Nout - n)
+                                                     : bf16x8{};
+            }
+        }
+      }
+    }
 #pragma unroll
     for (int j = 0; j < S::FM; ++j) {
       const int m = m0 + wm * S::TM + j * 32 + frow;
@@ -805,7 +828,8 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
 #pragma unroll
                     for (int e = 0; e < 8; ++e) r[e] = to_f32(rv[e]);
                   } else {
-                    load8(a.resid + (int64_t)m * a.ldr + n, r, valid);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) r[e] = to_f32(rres[j][i][gp][e]);
                   }
                 }
 #pragma unroll

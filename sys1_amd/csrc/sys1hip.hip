@@ -90,6 +90,8 @@ struct Context {
   int chain_wait_us = 20000;  // real time a dependency wait may take before it gives up
   int chain_extra = 0;
   int chain_occ = 0;         // resident chain workgroups per CU
+  unsigned long long* chain_trace = nullptr;  // optional timeline buffer (sys1hip_set_chain_trace)
+  int64_t chain_trace_bytes = 0;
   int forced_kernel = -1;
   int forced_grid = 0;
   int forced_dp = -1;
@@ -1247,6 +1249,7 @@ int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t
   a.wait_us = c->chain_wait_us;
   a.dep_extra = c->chain_extra;
   const int grid = c->cus * c->chain_occ;
+  a.trace = c->chain_trace && c->chain_trace_bytes >= (int64_t)grid * kChainTraceTiles * 32 ? c->chain_trace : nullptr;
   hipLaunchKernelGGL(reinterpret_cast<void (*)(ChainArgs)>(const_cast<void*>(ck.fn)), dim3((unsigned)grid),
                      dim3(ck.threads), 0, c->stream, a);
   HIP_TRY(hipGetLastError());
@@ -1281,6 +1284,14 @@ int sys1hip_chain_status(void* ctx, int32_t* flags) {
   HIP_TRY(hipMemcpy(&v, c->chain + kChainBankWords, sizeof(v), hipMemcpyDeviceToHost));
   if (v) HIP_TRY(hipMemset(c->chain + kChainBankWords, 0, sizeof(v)));
   *flags = (int32_t)v;
+  return SYS1HIP_OK;
+}
+
+int sys1hip_set_chain_trace(void* ctx, void* buffer, int64_t bytes) {
+  if (!ctx) return fail(SYS1HIP_EINVAL, "sys1hip_set_chain_trace: null context");
+  Context* c = static_cast<Context*>(ctx);
+  c->chain_trace = static_cast<unsigned long long*>(buffer);
+  c->chain_trace_bytes = buffer ? bytes : 0;
   return SYS1HIP_OK;
 }
 

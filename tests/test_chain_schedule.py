@@ -7,7 +7,9 @@ sys1_amd/csrc/chain.hip), without a device.
    dependencies (the previous projection's tiles on its row panel) come
    earlier in its queue.
 2. A model of one launch's wave protocol -- compute wave 0 taking tiles and
-   publishing them with their readiness, the producer waves' issue cursor,
+   publishing them with their readiness, the compute waves counting a tile
+   a k-step into the next one (at once before a drain or the end), the
+   producer waves' issue cursor,
    decision, drain and end, and the barriers both sides meet -- run under
    random interleavings of many workgroups on the real queues: every
    workgroup's producer and compute waves meet the same barriers in the same
@@ -104,9 +106,18 @@ def _compute(L, xcc, wg):
     wg["read"].append(0)
     next_raw = next_id = -1
     poll = 0
+    pending = None
+
+    def release(t):
+        L.deps[(t[0], t[1])] = L.deps.get((t[0], t[1]), 0) + WAVES
+
     while True:
         assert wg["issued"] > s, "a k-tile's fragments read before it was issued"
-        if ckt == 0:
+        rel_at = 1 if kc > STAGES + 1 else 0
+        if pending is not None and ckt == rel_at:
+            release(pending)
+            pending = None
+        if ckt == rel_at:
             next_raw = L.grab(xcc)
         if ckt == max(0, kc - STAGES - 1):
             next_id = next_raw
@@ -128,7 +139,10 @@ def _compute(L, xcc, wg):
             ckt, s = ckt + 1, s + 1
             continue
         L.computed.append(ct)
-        L.deps[(ct[0], ct[1])] = L.deps.get((ct[0], ct[1]), 0) + WAVES
+        if streamed:
+            pending = ct  # counted a k-step into the next tile
+        else:
+            release(ct)
         if nid < 0:
             break
         if not streamed:
