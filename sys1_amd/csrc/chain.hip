@@ -125,6 +125,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
+  const uint64_t t_entry = a->trace ? wall_clock64() : 0;
   const int xcc = hw_xcc_id();
   const bool active = xcc < a->nxcd;
   int tiles_n[kChainMax];
@@ -467,7 +468,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
     bool drained = false;
     unsigned long long* const trace = a->trace;
     auto record = [&]() {
-      if (trace && wave == 0 && lane == 0 && n < kChainTraceTiles) {
+      if (trace && wave == 0 && lane == 0 && n < kChainTraceTiles - 1) {
         unsigned long long* r = trace + ((size_t)blockIdx.x * kChainTraceTiles + n) * 4;
         r[0] = (unsigned long long)cur_id | ((unsigned long long)q.xcc << 32) | ((unsigned long long)drained << 40);
         r[1] = t_start;
@@ -481,7 +482,16 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
     int next_id = -1;
     ChainTile next_tile{0, 0, 0};
     __syncthreads();  // B_start
-    if (trace) t_start = wall_clock64();
+    if (trace) {
+      t_start = wall_clock64();
+      if (wave == 0 && lane == 0) {  // the last record: kernel entry and first data in LDS
+        unsigned long long* r = trace + ((size_t)blockIdx.x * kChainTraceTiles + kChainTraceTiles - 1) * 4;
+        r[0] = 0xffffffffull;
+        r[1] = t_entry;
+        r[2] = t_start;
+        r[3] = 0;
+      }
+    }
     read(fr[0], 0, 0);
     read(fr[1], 0, 1);
     int stage = 0;

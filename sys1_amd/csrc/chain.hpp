@@ -41,7 +41,8 @@ struct ChainArgs {
   // Optional timeline (null: off): per workgroup, kChainTraceTiles records of
   // 4 x u64 {queue index | xcc << 32 | drained << 40, start, stores done,
   // projection | (epilogue start - start) << 8}, times on the 100 MHz
-  // constant clock.
+  // constant clock; the last record holds {~0, kernel entry, first k-tile
+  // in LDS, 0}.
   unsigned long long* trace;
 };
 constexpr int kChainTraceTiles = 64;
