@@ -717,7 +717,9 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
     // load behind a store to a possibly aliasing address would wait a whole
     // round trip each.  A lane reads exactly the elements it then writes, so
     // reading them all first is correct in place too.
-    constexpr bool kResRegs = epi_has_resid<E>() && !epi_gated(E) && E != kEpiRopeQkv;
+    // (Only for wave tiles of at most three 32x32 blocks: the larger ones
+    // have no registers to spare for the batch and would spill.)
+    constexpr bool kResRegs = epi_has_resid<E>() && !epi_gated(E) && E != kEpiRopeQkv && S::FM * S::FN <= 3;
     bf16x8 rres[kResRegs ? S::FM : 1][kResRegs ? S::FN : 1][2];
     if constexpr (kResRegs) {
       if (!(kResLds && res_in_lds)) {
@@ -827,9 +829,11 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
                         res_lds + ((m - m0) * BN + (n - n0)) * 2);
 #pragma unroll
                     for (int e = 0; e < 8; ++e) r[e] = to_f32(rv[e]);
-                  } else {
+                  } else if constexpr (kResRegs) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) r[e] = to_f32(rres[j][i][gp][e]);
+                  } else {
+                    load8(a.resid + (int64_t)m * a.ldr + n, r, valid);
                   }
                 }
 #pragma unroll
