@@ -407,7 +407,16 @@ Plan price_plans(const Context* c, int64_t M0, int64_t N, int64_t K, bool wide, 
                              (2 * N * K <= kRereadWeightBytes && cdiv(M, e.bm) <= 2);
       if (e.streamk && M > e.bm && ((M <= 256 && !reread_ok) || cdiv(M, e.bm) * cdiv(N, e.bn) >= c->cus))
         continue;
-      if (!e.streamk && M <= 128) continue;
+      // Tile shapes up to 128 tokens only above 64 tokens (a 128-row tile at
+      // least half used) and as one round of whole tiles over at least two
+      // thirds of the CUs: the weight then streams with no
+      // split tile to fix up (measured: Qwen3.5-27B gate_up at M = 128,
+      // 182 tiles of 128x192, 76.0 us against 81.6-84.1 us on the stream-K
+      // hybrid whose 16 split tiles are summed after the stream).
+      const int64_t whole = cdiv(M, e.bm) * cdiv(N, e.bn);
+      if (!e.streamk && M <= 128 &&
+          !(M > 64 && cdiv(M, e.bm) == 1 && whole <= (int64_t)c->cus && 3 * whole >= 2 * (int64_t)c->cus))
+        continue;
     }
     const int64_t gmax = max_grid(c, id, epi, M, N, K);
     if (c->forced_grid > 0) {
