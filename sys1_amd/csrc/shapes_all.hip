@@ -1,7 +1,7 @@
 // Every GEMM kernel of libsys1hip in one translation unit: the tile and
 // skinny shapes of shapes.def, expanded here instead of one file per shape.
 // For builds that want a fixed list of sources (a Rust build.rs, a Makefile):
-//   hipcc --offload-arch=gfx950 ... -shared sys1hip.hip shapes_all.hip
+//   hipcc --offload-arch=gfx950 ... -shared sys1hip.hip chain.hip shapes_all.hip
 // links the same library as sys1_amd/build.py, which compiles the shapes in
 // parallel, one per translation unit, from the same list.
 #include "gemm_tile.hpp"
