@@ -48,6 +48,7 @@
 // the word with sys1hip_chain_status.
 #include "chain.hpp"
 #include "gemm_tile.hpp"
+#include "skinny.hpp"
 
 namespace sys1 {
 
@@ -600,6 +601,255 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
     }
   }
 }
+
+// ---------------------------------------------------------------------------
+// The same chain for a few dozen tokens: a weight stream.  Up to 64 token rows
+// (one 64-row tile), every projection is a stream of its weight, and a
+// projection's rows depend on all of the previous projection's output
+// columns.  Work items are 32-column blocks of a projection over the whole K
+// (the skinny kernels' tile: K split over the NW waves of a workgroup, f32
+// partials summed in LDS in wave order), taken from one queue in
+// projection-major order by every CU.  A workgroup issues the loads of its
+// item's weight share first -- they depend on nothing -- and only then waits
+// until the previous projection's items are all done, so the weight of the
+// next projection streams in while the current one finishes.  Outputs and
+// activations cross XCDs here, so they move with the agent-coherent policy
+// (sc1: stores write through, loads bypass stale L2 lines), as the stream-K
+// partials do; the dependency counters are agent-scope atomics.
+constexpr int kPolicySc1 = 16;
+
+template <int FM, int FN, int NW, int SMAX, int G>
+__global__ __launch_bounds__(NW * 64) void stream_chain_kernel(ChainArgs) {
+  const KArgs a = (KArgs)__builtin_amdgcn_kernarg_segment_ptr();
+  constexpr int BM = FM * 16, BN = FN * 16;
+  constexpr int kRowF32 = BN + 4;
+  static_assert(NW * BM * kRowF32 * 4 <= 160 * 1024, "LDS budget");
+  static_assert(FN % 2 == 0, "whole 32-row gate/up groups per item");
+  __shared__ __attribute__((aligned(16))) float red[NW * BM * kRowF32];
+  __shared__ int slot[2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, q = lane >> 4;
+  unsigned* const head = a->bank;
+  unsigned* const done = a->bank + kChainXcdMax;
+  unsigned* const aborted = a->bank + kChainXcdMax + 1;
+  unsigned* const deps = a->bank + kChainHeader;  // items finished, per projection
+  int total = 0;
+#pragma unroll
+  for (int p = 0; p < kChainMax; ++p) total += p < a->nproj ? a->proj[p].tiles_n : 0;
+  auto decode = [&](int i, int& p, int& cb) {
+    p = 0;
+    int base = 0;
+#pragma unroll
+    for (int pp = 0; pp + 1 < kChainMax; ++pp) {
+      const int c = a->proj[pp].tiles_n;
+      if (p == pp && pp + 1 < a->nproj && i >= base + c) {
+        base += c;
+        p = pp + 1;
+      }
+    }
+    cb = i - base;
+  };
+  auto grab = [&]() -> unsigned {
+    unsigned i = 0xffffffffu;
+    if (lane == 0) i = __hip_atomic_fetch_add(head, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return i;
+  };
+  auto id_of = [&](unsigned raw) -> int {
+    const int i = (int)__builtin_amdgcn_readfirstlane(raw);
+    return i >= 0 && i < total ? i : -1;
+  };
+  // Bounded wait (wave 0) for all items of projection p: as the tile chain's.
+  auto wait_items = [&](int p) {
+    const unsigned need = (unsigned)(a->proj[p].tiles_n + a->dep_extra);
+    if (atomic_load_agent(deps + p) >= need || atomic_load_agent(aborted)) return;
+    const uint64_t t0 = wall_clock64();
+    const uint64_t budget = (uint64_t)a->wait_us * 100;
+    for (int n = 1; atomic_load_agent(deps + p) < need; ++n) {
+      if (wall_clock64() - t0 > budget || ((n & 15) == 0 && atomic_load_agent(aborted))) {
+        if (lane == 0) {
+          __hip_atomic_store(aborted, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_or(a->err, kChainErrTimeout, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+      }
+      __builtin_amdgcn_s_sleep(4);
+    }
+  };
+
+  if (wave == 0) {
+    const int id = id_of(grab());
+    if (lane == 0) slot[0] = id;
+  }
+  __syncthreads();
+  for (int n = 0;; ++n) {
+    const int id = __builtin_amdgcn_readfirstlane(slot[n & 1]);
+    if (id < 0) break;
+    int p, cb;
+    decode(id, p, cb);
+    const ChainProj P = proj_at(a, p);
+    const int n0 = cb * BN;
+    unsigned next_raw = 0xffffffffu;
+    if (wave == 0) next_raw = grab();  // (consumed at the item's end)
+
+    // ---- this wave's share of K: k-steps [s0, s1) of 32
+    const int ksteps = (P.K + 31) / 32;
+    const int s0 = wave * ksteps / NW, s1 = (wave + 1) * ksteps / NW;
+    const rsrc_t wr = make_rsrc_uniform(P.w, 0x7ffffff0);
+    const rsrc_t xr = make_rsrc_uniform(P.x, 0x7ffffff0);
+    unsigned wo[FN], xo[FM];
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const int nr = min(n0 + i * 16 + r16, P.N - 1);
+      wo[i] = P.w_kt ? (unsigned)((nr / kBlkRows) * P.w_kt * kBlkBytes + (nr % kBlkRows) * (kBlkK * 2) + q * 16)
+                     : (unsigned)((int64_t)nr * P.ldw * 2 + q * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < FM; ++j) xo[j] = (unsigned)((int64_t)min(j * 16 + r16, a->M - 1) * P.ldx * 2 + q * 16);
+    auto wstep = [&](int st) { return P.w_kt ? (st >> 1) * kBlkBytes + (st & 1) * 64 : st * 64; };
+    // The weight share first: it depends on nothing.  (A wave without
+    // k-steps -- K below 32 NW -- issues out-of-range loads at offset 0,
+    // never a negative one.)
+    i32x4 wreg[SMAX][FN];
+#pragma unroll
+    for (int u = 0; u < SMAX; ++u) {
+      const int st = s0 + u;
+      const bool ok = st < s1 && st * 32 + q * 8 < P.K;
+      const int sw = __builtin_amdgcn_readfirstlane(wstep(max(0, min(st, s1 - 1))));
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+        wreg[u][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, ok ? (int)wo[i] : (int)kOutOfRange, sw, 0);
+    }
+    // Then the dependency: every item of the previous projection.
+    if (p > 0 && wave == 0) wait_items(p - 1);
+    __syncthreads();
+    f32x4 acc[FN][FM];
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int g = 0; g < SMAX; g += G) {
+      if (s0 + g < s1) {
+        i32x4 xreg[G][FM];
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+          const int st = s0 + g + u;
+          const bool ok = g + u < SMAX && st < s1 && st * 32 + q * 8 < P.K;
+          const int so = __builtin_amdgcn_readfirstlane(max(0, min(st, s1 - 1)) * 64);
+#pragma unroll
+          for (int j = 0; j < FM; ++j)
+            xreg[u][j] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? (int)xo[j] : (int)kOutOfRange, so, kPolicySc1);
+        }
+#pragma unroll
+        for (int u = 0; u < G; ++u)
+          if (g + u < SMAX)
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+              for (int j = 0; j < FM; ++j) acc[i][j] = mfma16(wreg[g + u][i], xreg[u][j], acc[i][j]);
+      }
+    }
+    // Partials to LDS (wave w's block (i, j): rows 16 j + l % 16, columns
+    // 16 i + 4 (l / 16) .. + 3), summed below in wave order.
+    float* mine = red + wave * BM * kRowF32;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j)
+        *reinterpret_cast<f32x4*>(mine + (j * 16 + r16) * kRowF32 + i * 16 + 4 * q) = acc[i][j];
+    __syncthreads();
+    // Epilogue: one thread per 8 output columns of a row.
+    const bool gated = P.epi == kEpiGeglu || P.epi == kEpiSwiglu;
+    const int kVecs = gated ? BN / 16 : BN / 8;
+    const int out_n0 = gated ? n0 / 2 : n0;
+    const rsrc_t yr = make_rsrc_uniform(P.y, 0x7ffffff0);
+    const rsrc_t rr = make_rsrc_uniform(P.epi == kEpiResidual ? P.resid : P.y, 0x7ffffff0);
+    for (int t = tid; t < BM * kVecs; t += NW * 64) {
+      const int r = t / kVecs, c0 = (t % kVecs) * 8;
+      if (r >= a->M) continue;
+      const int nn = out_n0 + c0;
+      if (nn >= P.Nout) continue;  // (Nout % 8 == 0: whole 16-byte vectors)
+      const int pc = gated ? (c0 / 16) * 32 + c0 % 16 : c0;
+      float v[8], gu[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = gu[e] = 0.0f;
+      for (int ww = 0; ww < NW; ++ww) {
+        const float* row = red + (ww * BM + r) * kRowF32;
+        const f32x4 p0 = *reinterpret_cast<const f32x4*>(row + pc);
+        const f32x4 p1 = *reinterpret_cast<const f32x4*>(row + pc + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] += p0[e];
+          v[4 + e] += p1[e];
+        }
+        if (gated) {
+          const f32x4 u0 = *reinterpret_cast<const f32x4*>(row + pc + 16);
+          const f32x4 u1 = *reinterpret_cast<const f32x4*>(row + pc + 20);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            gu[e] += u0[e];
+            gu[4 + e] += u1[e];
+          }
+        }
+      }
+      bf16x8 o;
+      const unsigned yoff = (unsigned)(((int64_t)r * P.ldy + nn) * 2);
+      if (P.epi == kEpiGeglu) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = to_bf16(epi_gate<kEpiGeglu>(v[e], gu[e]));
+      } else if (P.epi == kEpiSwiglu) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = to_bf16(epi_gate<kEpiSwiglu>(v[e], gu[e]));
+      } else if (P.epi == kEpiResidual) {
+        const bf16x8 rv = __builtin_bit_cast(
+            bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rr, (int)(((int64_t)r * P.ldr + nn) * 2), 0, kPolicySc1));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = to_bf16(epi_apply<kEpiResidual>(v[e], 0.0f, to_f32(rv[e])));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = to_bf16(epi_apply<kEpiNone>(v[e], 0.0f, 0.0f));
+      }
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, o), yr, (int)yoff, 0, kPolicySc1);
+    }
+    // The item is done once every thread's stores are: count it, publish
+    // the next item.
+    vm_wait<0>();
+    __syncthreads();
+    if (wave == 0) {
+      const int nid = id_of(next_raw);
+      if (lane == 0) {
+        __hip_atomic_fetch_add(deps + p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        slot[(n + 1) & 1] = nid;
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- the end: the last workgroup checks the queue and clears the bank
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (wave == 0) {
+    unsigned prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev == gridDim.x - 1) {
+      if (lane == 0 && (int)atomic_load_agent(head) < total)
+        __hip_atomic_fetch_or(a->err, kChainErrUndrained, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int words = kChainHeader + a->nproj;
+      for (int i = lane; i < words; i += 64)
+        __hip_atomic_store(a->bank + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// The weight-streaming chain's shape: 64 token rows x 32 columns per item,
+// K over 12 waves (three per SIMD, 170 registers each), at most 7 k-steps of
+// 32 per wave (K <= 2688), activations loaded 4 k-steps at a time.
+const ChainKernel kStreamChainKernel = {
+    reinterpret_cast<const void*>(&stream_chain_kernel<4, 2, 12, 7, 4>), 64, 32, 7 * 32 * 12, 12 * 64};
 
 // The chain's tile shape: ModernBERT-base's output projections' shape
 // (N = 768 -> four 192-wide tiles), eight 32 x 96 compute waves and four

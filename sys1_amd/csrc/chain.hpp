@@ -93,8 +93,11 @@ struct XcdQueue {
 
 struct ChainKernel {
   const void* fn;
-  int bm, bn, stages, threads;
+  int bm, bn;
+  int stages;  // tile chain: LDS stages; weight-streaming chain: the largest K it takes
+  int threads;
 };
-extern const ChainKernel kChainKernel;
+extern const ChainKernel kChainKernel;        // tile chain (128 x 192 tiles)
+extern const ChainKernel kStreamChainKernel;  // weight-streaming chain (M <= 64)
 
 }  // namespace sys1

@@ -90,6 +90,7 @@ struct Context {
   int chain_wait_us = 20000;  // real time a dependency wait may take before it gives up
   int chain_extra = 0;
   int chain_occ = 0;         // resident chain workgroups per CU
+  int stream_chain_occ = 0;  // the same for the weight-streaming chain
   unsigned long long* chain_trace = nullptr;  // optional timeline buffer (sys1hip_set_chain_trace)
   int64_t chain_trace_bytes = 0;
   int forced_kernel = -1;
@@ -642,6 +643,9 @@ int sys1hip_init(int device, void** out) {
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&c->chain_occ, kChainKernel.fn, kChainKernel.threads, 0) !=
       hipSuccess)
     c->chain_occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&c->stream_chain_occ, kStreamChainKernel.fn,
+                                                   kStreamChainKernel.threads, 0) != hipSuccess)
+    c->stream_chain_occ = 0;
   (void)hipGetLastError();
   *out = c;
   return SYS1HIP_OK;
@@ -1202,6 +1206,15 @@ int sys1hip_pack_gated_weight(void* ctx, const uint16_t* w, uint16_t* packed, in
 
 // ---- projection chains (chain.hip)
 
+// Whether a chain runs as a weight stream: up to kStreamChainKernel.bm
+// tokens, every K within its reach.
+bool stream_chain_fits(const sys1hip_chain_proj* proj, int count, int64_t M) {
+  if (M > kStreamChainKernel.bm) return false;
+  for (int p = 0; p < count; ++p)
+    if (proj[p].K > kStreamChainKernel.stages) return false;
+  return true;
+}
+
 int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t count, int64_t M) {
   static const char* who = "sys1hip_linear_chain_bf16";
   if (!ctx) return fail(SYS1HIP_EINVAL, "%s: null context", who);
@@ -1209,8 +1222,12 @@ int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t
     return fail(SYS1HIP_EINVAL, "%s: %d projections (1..%d)", who, (int)count, kChainMax);
   if (M < 0) return fail(SYS1HIP_EINVAL, "%s: M=%lld", who, (long long)M);
   Context* c = static_cast<Context*>(ctx);
-  const ChainKernel& ck = kChainKernel;
-  const int64_t panels = cdiv(M, ck.bm);
+  // Up to 64 tokens the chain is a weight stream (stream_chain_kernel: 32-
+  // column items over the whole K, every CU); above, 128 x 192 tiles on row
+  // panels (chain_kernel).
+  const bool stream = stream_chain_fits(proj, count, M);
+  const ChainKernel& ck = stream ? kStreamChainKernel : kChainKernel;
+  const int64_t panels = stream ? 1 : cdiv(M, ck.bm);
   if (panels > kChainMaxPanels)
     return fail(SYS1HIP_ERANGE, "%s: M=%lld above %lld tokens", who, (long long)M, (long long)kChainMaxPanels * ck.bm);
   ChainArgs a{};
@@ -1223,7 +1240,7 @@ int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t
     if (epi != kEpiNone && epi != kEpiResidual && epi != kEpiGeglu && epi != kEpiSwiglu)
       return fail(SYS1HIP_EINVAL, "%s: projection %d: epilogue flags %d (none, residual, GeGLU or SwiGLU)", who, p,
                   q.epilogue);
-    if (q.K % kBlkK || q.K / kBlkK < ck.stages)
+    if (!stream && (q.K % kBlkK || q.K / kBlkK < ck.stages))
       return fail(SYS1HIP_EINVAL, "%s: projection %d: K=%lld must be a multiple of %d and at least %d", who, p,
                   (long long)q.K, kBlkK, kBlkK * ck.stages);
     const int64_t nout = epi_gated(epi) ? q.N / 2 : q.N;
@@ -1231,8 +1248,13 @@ int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t
         (nout % 8 || q.ldr % 8 || !aligned16(q.residual) || 2 * (M * q.ldr + nout) >= 0x7ffffff0ll))
       return fail(SYS1HIP_EALIGN, "%s: projection %d: the residual needs Nout and ldr multiples of 8, 16-byte "
                   "alignment and fewer than 2 GiB of rows", who, p);
-    if (2 * (int64_t)ck.bm * q.ldx + 2 * q.K >= 0x7ffffff0ll || (!(q.epilogue & SYS1HIP_EPI_BLOCKED_W) &&
-                                                                2 * (int64_t)ck.bn * q.ldw >= 0x7ffffff0ll))
+    if (stream && (nout % 8 || q.ldy % 8 || !aligned16(q.y) || 2 * (M * q.ldy + nout) >= 0x7ffffff0ll ||
+                   2 * (M * q.ldx + q.K) >= 0x7ffffff0ll ||
+                   (q.epilogue & SYS1HIP_EPI_BLOCKED_W ? blocked_bytes(q.N, q.K) : 2 * q.N * q.ldw) >= 0x7ffffff0ll))
+      return fail(SYS1HIP_EALIGN, "%s: projection %d: a chain of up to %d tokens needs Nout and ldy multiples of 8, "
+                  "16-byte aligned y and operands below 2 GiB", who, p, kStreamChainKernel.bm);
+    if (!stream && (2 * (int64_t)ck.bm * q.ldx + 2 * q.K >= 0x7ffffff0ll ||
+                    (!(q.epilogue & SYS1HIP_EPI_BLOCKED_W) && 2 * (int64_t)ck.bn * q.ldw >= 0x7ffffff0ll)))
       return fail(SYS1HIP_ERANGE, "%s: projection %d: leading dimension too large", who, p);
     ChainProj& P = a.proj[p];
     P.x = reinterpret_cast<const __bf16*>(q.x);
@@ -1248,7 +1270,8 @@ int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t
   if (M == 0) return SYS1HIP_OK;
   int rc = use_device(c);
   if (rc) return rc;
-  if (c->chain_occ < 1) return fail(SYS1HIP_EDEVICE, "%s: the chain kernel cannot be resident on this device", who);
+  const int occ = stream ? c->stream_chain_occ : c->chain_occ;
+  if (occ < 1) return fail(SYS1HIP_EDEVICE, "%s: the chain kernel cannot be resident on this device", who);
   a.bank = c->chain;
   a.err = c->chain + kChainBankWords;
   a.nproj = count;
@@ -1257,8 +1280,9 @@ int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t
   a.nxcd = kChainXcdMax;
   a.wait_us = c->chain_wait_us;
   a.dep_extra = c->chain_extra;
-  const int grid = c->cus * c->chain_occ;
-  a.trace = c->chain_trace && c->chain_trace_bytes >= (int64_t)grid * kChainTraceTiles * 32 ? c->chain_trace : nullptr;
+  const int grid = c->cus * occ;
+  a.trace = !stream && c->chain_trace && c->chain_trace_bytes >= (int64_t)grid * kChainTraceTiles * 32
+                ? c->chain_trace : nullptr;
   hipLaunchKernelGGL(reinterpret_cast<void (*)(ChainArgs)>(const_cast<void*>(ck.fn)), dim3((unsigned)grid),
                      dim3(ck.threads), 0, c->stream, a);
   HIP_TRY(hipGetLastError());

@@ -310,3 +310,58 @@ def test_every_access_of_every_tile_stays_inside_its_operand(name, M, blocked):
             for n in cols:
                 assert n + 8 <= nout
                 assert (last_row * ldy + n + 8) * 2 <= ((M - 1) * ldy + nout) * 2
+
+
+@pytest.mark.parametrize("M", [1, 17, 64])
+@pytest.mark.parametrize("blocked", [False, True])
+@pytest.mark.parametrize("name,chain", [
+    ("modernbert-large", [(1024, 1024, "res"), (5248, 1024, "gated"), (1024, 2624, "res"), (3072, 1024, "none")]),
+    ("modernbert-base", [(768, 768, "res"), (2304, 768, "gated"), (768, 1152, "res"), (2304, 768, "none")]),
+    ("short-k", [(96, 64, "none"), (64, 40, "res")])])
+def test_weight_streaming_chain_accesses_stay_inside_their_operands(M, blocked, name, chain):
+    """The weight-streaming chain (up to 64 tokens: 32-column items over the
+    whole K, K split over 12 waves of at most 7 k-steps of 32): every byte
+    offset its loads and stores form, restated from the kernel -- weight rows
+    clamped to N, token rows to M, k-chunks past K out of range, no negative
+    k-step offset for a wave without k-steps -- lies inside the operand."""
+    NW, SMAX, BN, BM = 12, 7, 32, 64
+    OOR = 0x80000000
+    for N, K, kind in chain:
+        assert K <= SMAX * 32 * NW
+        ldx, ldw = K + 8, K + 24
+        w_kt = -(-K // 64)
+        nout = N // 2 if kind == "gated" else N
+        ldy = nout + 16
+        ksteps = -(-K // 32)
+        for cb in range(-(-N // BN)):
+            n0 = cb * BN
+            for wave in range(NW):
+                s0, s1 = wave * ksteps // NW, (wave + 1) * ksteps // NW
+                for lane in range(64):
+                    r16, q = lane & 15, lane >> 4
+                    for u in range(SMAX):
+                        st = s0 + u
+                        ok = st < s1 and st * 32 + q * 8 < K
+                        sc = max(0, min(st, s1 - 1))
+                        assert sc >= 0
+                        if not ok:
+                            continue  # out-of-range offset: no access
+                        for i in range(2):
+                            nr = min(n0 + i * 16 + r16, N - 1)
+                            if blocked:
+                                off = (nr // 32) * w_kt * 4096 + (nr % 32) * 128 + q * 16 + (sc >> 1) * 4096 + (sc & 1) * 64
+                                assert off + 16 <= -(-N // 32) * w_kt * 4096
+                            else:
+                                off = nr * ldw * 2 + q * 16 + sc * 64
+                                assert off + 16 <= ((N - 1) * ldw + K) * 2
+                        for j in range(BM // 16):
+                            xo = min(j * 16 + r16, M - 1) * ldx * 2 + q * 16 + sc * 64
+                            assert xo + 16 <= ((M - 1) * ldx + K) * 2
+            # epilogue: rows r < M, 8-column vectors n < Nout
+            vecs = BN // 16 if kind == "gated" else BN // 8
+            out_n0 = n0 // 2 if kind == "gated" else n0
+            for t in range(BM * vecs):
+                r, c0 = t // vecs, (t % vecs) * 8
+                if r >= M or out_n0 + c0 >= nout:
+                    continue
+                assert (r * ldy + out_n0 + c0 + 8) * 2 <= ((M - 1) * ldy + nout) * 2

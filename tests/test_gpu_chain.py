@@ -263,3 +263,108 @@ def test_chain_stack_against_the_oracle_chain(dev, orc):
     print(f"[gpu]   final hidden vs bf16-rounding oracle chain {rel:.3e}; oracle chains differ by {spread:.3e}",
           flush=True)
     assert rel < 4 * spread
+
+
+# ---- up to 64 tokens: the weight-streaming chain (32-column items over the
+# whole K, K split over the waves, every CU) -- not the tile kernels' summation
+# order, so checked against the oracle, not bit for bit.
+
+@pytest.mark.parametrize("M", [1, 17, 64])
+def test_weight_streaming_chain_launch_against_the_oracle(dev, orc, M):
+    """ModernBERT-large (config 3) attn.Wo(+residual) -> Wi+GeGLU ->
+    mlp.Wo(+residual) -> Wqkv in one launch at small M, blocked weights:
+    each output against the oracle's f32 projection of the GPU chain's own
+    inputs."""
+    from sys1_amd import _lib
+    from sys1_amd.linear import pack_blocked_weight, pack_gated_weight
+    H, I = 1024, 2624
+    print(f"[gpu] weight-streaming chain modernbert-large M={M}", flush=True)
+    qkv_np = orc.round_bf16(orc.fill_normal((M, 3 * H), 3))
+    h0_np = orc.round_bf16(orc.fill_normal((M, H), 4))
+    w = [orc.round_bf16(orc.fill_normal(s, 20 + i, 0.02))
+         for i, s in enumerate([(H, H), (2 * I, H), (H, I), (3 * H, H)])]
+    qkv = to_gpu_bf16(qkv_np, torch)
+    h = to_gpu_bf16(h0_np, torch)
+    act = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
+    wg = [to_gpu_bf16(v, torch) for v in w]
+    wg[1] = pack_gated_weight(wg[1], dev)
+    wb = [pack_blocked_weight(v, dev) for v in wg]
+    qkv_out = torch.empty(M, 3 * H, dtype=torch.bfloat16, device="cuda")
+    B = _lib.EPI_BLOCKED_W
+
+    def cp(x, wi, y, epi, N, K, res=None):
+        return _lib.ChainProj(x.data_ptr(), x.stride(0), wb[wi].data_ptr(), K,
+                              res.data_ptr() if res is not None else None, res.stride(0) if res is not None else 0,
+                              y.data_ptr(), y.stride(0), N, K, epi | B)
+    projs = [cp(qkv[:, 2 * H:], 0, h, _lib.EPI_RESIDUAL, H, H, res=h),
+             cp(h, 1, act, _lib.EPI_GEGLU, 2 * I, H),
+             cp(act, 2, h, _lib.EPI_RESIDUAL, H, I, res=h),
+             cp(h, 3, qkv_out, _lib.EPI_NONE, 3 * H, H)]
+    _chain_launch(dev, projs, M)
+    torch.cuda.synchronize()
+    assert dev.chain_status() == 0
+    h1_ref = orc.linear_f32(np.ascontiguousarray(qkv_np[:, 2 * H:]), w[0]) + h0_np
+    act_np = to_np(act)
+    assert_parity(act_np, orc.geglu(orc.linear_f32(orc.round_bf16(h1_ref), w[1])), f"Wi+GeGLU M={M}")
+    h2_np = to_np(h)
+    assert_parity(h2_np, orc.linear_f32(act_np, w[2]) + orc.round_bf16(h1_ref), f"mlp.Wo M={M}")
+    assert_parity(to_np(qkv_out), orc.linear_f32(h2_np, w[3]), f"Wqkv M={M}")
+
+
+@pytest.mark.parametrize("M", [16, 64])
+def test_weight_streaming_chain_stack_against_per_projection_and_oracle(dev, orc, M):
+    """The ModernBERT-large stack (4 layers) with chains at small M against
+    the per-projection stack (skinny kernels, another summation order) and
+    the oracle chain that rounds where the GPU path rounds; run twice, the
+    same bits both times."""
+    from sys1_amd.stacks import ProjectionStack, modernbert
+    import test_gpu_stack as T
+    cfg = modernbert(1024, 2624, 4, "modernbert-large-4")
+    print(f"[gpu] weight-streaming chain stack modernbert-large 4 layers M={M}", flush=True)
+    x = orc.fill_normal((M, 1024), 51)
+    ws = T._weights(orc, cfg, 400)
+    wg = [[to_gpu_bf16(w, torch) for w in l] for l in ws]
+    a = ProjectionStack(cfg, dev, M, weights=wg, blocked=True, chain=True)
+    b = ProjectionStack(cfg, dev, M, weights=wg, blocked=True)
+    xg = to_gpu_bf16(x, torch)
+    ya = a.forward(xg, M).clone()
+    ya2 = a.forward(xg, M).clone()
+    yb = b.forward(xg, M).clone()
+    torch.cuda.synchronize()
+    assert dev.chain_status() == 0
+    assert torch.equal(ya.view(torch.int16), ya2.view(torch.int16))
+    emul = T._oracle_chain_bf16(orc, cfg, x, ws, None)
+    f32 = T._oracle_chain(orc, cfg, x, ws, None)
+    spread, _ = parity(emul, f32)
+    ra, _ = parity(to_np(ya), emul)
+    rb, _ = parity(to_np(yb), emul)
+    print(f"[gpu]   vs bf16-rounding oracle chain: chain {ra:.3e}, per-projection {rb:.3e}; oracle chains "
+          f"differ by {spread:.3e}", flush=True)
+    assert ra < max(4 * spread, 1e-2) and rb < max(4 * spread, 1e-2)
+
+
+def test_weight_streaming_chain_bounded_wait(dev, orc):
+    """The weight-streaming chain's waits, forced to expire from the host:
+    the launch finishes and reports it; the next launch is clean."""
+    from sys1_amd.stacks import ProjectionStack, modernbert
+    cfg = modernbert(1024, 2624, 2, "modernbert-large-2")
+    M = 32
+    ws = [[(torch.randn(p.N, p.K, device="cuda") * 0.02).to(torch.bfloat16) for p in layer]
+          for layer in cfg.layers]
+    a = ProjectionStack(cfg, dev, M, weights=ws, blocked=True, chain=True)
+    x = to_gpu_bf16(orc.fill_normal((M, 1024), 7), torch)
+    ref = a.forward(x, M).clone()
+    torch.cuda.synchronize()
+    assert dev.chain_status() == 0
+    dev.set_chain_wait(wait_us=200, extra=1 << 20)
+    try:
+        print("[gpu] weight-streaming chain with unreachable dependencies", flush=True)
+        a.forward(x, M)
+        flags = dev.chain_status()
+    finally:
+        dev.set_chain_wait()
+    assert flags & 1
+    again = a.forward(x, M).clone()
+    torch.cuda.synchronize()
+    assert dev.chain_status() == 0
+    assert torch.equal(again.view(torch.int16), ref.view(torch.int16))
