@@ -86,6 +86,10 @@ def parse():
     ap.add_argument("--trace-summary", metavar="CSV",
                     help="reduce a rocprofv3 kernel_trace.csv of a bench run (with --workload, --tokens) "
                          "to per-projection kernel durations and their HBM / MFMA rates, and exit")
+    ap.add_argument("--chain-timeline", action="store_true",
+                    help="with --chain on: after the warm-up, record the in-kernel timeline of one chain "
+                         "launch (the middle layer's; sys1hip_set_chain_trace), print its per-projection "
+                         "summary as markdown and exit")
     ap.add_argument("--pmc-summary", nargs="+", metavar="CSV",
                     help="reduce rocprofv3 counter_collection.csv files to per-kernel averages "
                          "per dispatch and exit (no GPU use)")
@@ -111,6 +115,89 @@ def pmc_summary(paths: list[str]) -> None:
         n = max(len(v) for v in cs.values())
         vals = ", ".join(f"{c}={sum(v) / len(v):.6g}" for c, v in sorted(cs.items()))
         print(f"{n:6d} dispatches | {vals} | {name[:160]}")
+
+
+def chain_timeline(dev, launches, M: int) -> None:
+    """One chain launch with the in-kernel trace on: every workgroup's
+    wave 0 records each item or tile it runs (100 MHz constant clock).
+    Prints per projection the start / dependency / end windows (weight-
+    streaming chain, M <= 64) or the tile, k-loop and epilogue times (tile
+    chain), as markdown."""
+    import ctypes
+    import collections
+    import numpy as np
+    import torch
+    from sys1_amd import _lib
+    from sys1_amd.stacks import STREAM_CHAIN_MAX_M, STREAM_CHAIN_MAX_K
+    chains = [c for c in launches if isinstance(c[0], tuple)]
+    if not chains:
+        raise SystemExit("--chain-timeline: no chain launch in this stack (use --chain on)")
+    projs, fn, a = chains[len(chains) // 2]
+    names = [p.name for p in projs]
+    stream = M <= STREAM_CHAIN_MAX_M and all(p.K <= STREAM_CHAIN_MAX_K for p in projs)
+    slots, per = 1024, 64
+    buf = torch.zeros(slots * per * 4, dtype=torch.int64, device="cuda:0")
+    L = dev._L
+    _lib.check(L.sys1hip_set_chain_trace(dev.ctx, ctypes.c_void_p(buf.data_ptr()), buf.numel() * 8), dev.ctx)
+    try:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        dev.follow_torch_stream()
+        e0.record()
+        if fn(*a):
+            raise RuntimeError("chain launch failed")
+        e1.record()
+        torch.cuda.synchronize()
+        flags = dev.chain_status()
+    finally:
+        _lib.check(L.sys1hip_set_chain_trace(dev.ctx, None, 0), dev.ctx)
+    t = buf.view(slots, per, 4).cpu().numpy().astype(np.uint64)
+    us = lambda ticks: ticks / 100.0
+    q = lambda v: f"{np.min(v):.1f} / {np.median(v):.1f} / {np.max(v):.1f}"
+    print(f"chain {' -> '.join(names)}, M = {M}, "
+          f"{'weight-streaming chain' if stream else 'tile chain'}: launch {e0.elapsed_time(e1) * 1e3:.1f} us "
+          f"(HIP events), status {flags}")
+    if stream:
+        recs = [(wg, k, int(r[0]) >> 32, int(r[1]), int(r[2]), int(r[3]))
+                for wg in range(slots) for k in range(per) for r in [t[wg, k]] if r[3]]
+        t0 = min(r[3] for r in recs)
+        print(f"items {len(recs)}, workgroups {len(set(r[0] for r in recs))}, "
+              f"span {us(max(r[5] for r in recs) - t0):.1f} us, second-round items {sum(r[1] > 0 for r in recs)}")
+        print()
+        print("| projection | items | start (min / median / max, us) | dependency met | end | "
+              "work after the wait |")
+        print("|---|---:|---|---|---|---|")
+        for p in range(len(names)):
+            rs = [r for r in recs if r[2] == p]
+            st = [us(r[3] - t0) for r in rs]
+            dp = [us(r[4] - t0) for r in rs]
+            en = [us(r[5] - t0) for r in rs]
+            wk = [us(r[5] - r[4]) for r in rs]
+            print(f"| {names[p]} | {len(rs)} | {q(st)} | {q(dp)} | {q(en)} | {q(wk)} |")
+        return
+    recs, entries = [], []
+    for wg in range(slots):
+        for k in range(per):
+            r = t[wg, k]
+            if r[1] == 0 and r[2] == 0:
+                continue
+            if int(r[0]) == 0xffffffff:
+                entries.append((int(r[1]), int(r[2])))
+                continue
+            recs.append((wg, int(r[0]) >> 40 & 1, int(r[1]), int(r[2]), int(r[3]) & 0xff, us(int(r[3]) >> 8)))
+    t0 = min(e[0] for e in entries)
+    print(f"tiles {len(recs)}, workgroups {len(entries)}, span {us(max(r[3] for r in recs) - t0):.1f} us, "
+          f"tiles that waited for their dependency {sum(r[1] for r in recs)}, "
+          f"entry to first k-tile in LDS {q([us(e[1] - e[0]) for e in entries])} us")
+    print()
+    print("| projection | tiles | tile (mean, us) | k-loop (min / median / max) | epilogue (mean) | "
+          "first start / last end |")
+    print("|---|---:|---:|---|---:|---|")
+    for p in range(len(names)):
+        rs = [r for r in recs if r[4] == p]
+        d = [us(r[3] - r[2]) for r in rs]
+        kl = [r[5] for r in rs]
+        print(f"| {names[p]} | {len(rs)} | {np.mean(d):.1f} | {q(kl)} | {np.mean(d) - np.mean(kl):.1f} | "
+              f"{us(min(r[2] for r in rs) - t0):.1f} / {us(max(r[3] for r in rs) - t0):.1f} |")
 
 
 def trace_summary(path: str, workload: str, tokens: int | None) -> None:
@@ -379,6 +466,9 @@ def main():
     for s in range(args.warmup):
         stack.run_prepared(prepared[s % len(Ms)])
     torch.cuda.synchronize()
+    if args.chain_timeline:
+        chain_timeline(dev, prepared[0], Ms[0])
+        return
 
     # Optionally one HIP graph per prepared batch: the same kernel launches,
     # with the host's enqueue cost taken out of the step.  Every launch reads

@@ -101,6 +101,31 @@ __device__ __forceinline__ ChainProj proj_at(KArgs a, int p) {
 
 }  // namespace
 
+// Whether this workgroup is the launch's last to exit (wave 0 calls it; the
+// result is wave-uniform).  Exits are counted in two levels, per slot of
+// kStreamSlots workgroups and then per slot: same-address atomics serialise
+// (some 40 ns each, measured), and one counter for 256 exiting workgroups
+// would add microseconds to the launch's tail.  The last one clears the
+// exit counters; the caller clears the rest of the bank.
+__device__ bool chain_exit_last(unsigned* bank, int lane) {
+  unsigned* const exits = bank + kChainExitWords;
+  unsigned* const done = bank + kChainXcdMax;
+  const int es = (int)(blockIdx.x % kStreamSlots);
+  const unsigned members = (gridDim.x - es + kStreamSlots - 1) / kStreamSlots;
+  const unsigned groups = min(gridDim.x, (unsigned)kStreamSlots);
+  unsigned last = 0;
+  if (lane == 0) {
+    const unsigned prev =
+        __hip_atomic_fetch_add(exits + es * kStreamSlotStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == members - 1)
+      last = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1 == groups;
+  }
+  last = __builtin_amdgcn_readfirstlane(last);
+  if (last && lane < kStreamSlots)
+    __hip_atomic_store(exits + lane * kStreamSlotStride, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last != 0;
+}
+
 template <int BM, int BN, int WM, int WN, int STAGES, int PW>
 __global__ __launch_bounds__((WM * WN + PW) * 64)
 __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel(ChainArgs) {
@@ -134,7 +159,6 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
   for (int p = 0; p < kChainMax; ++p) tiles_n[p] = p < a->nproj ? CHAIN_FIELD(a, p, tiles_n) : 0;
   const XcdQueue q(active ? xcc : 0, a->nxcd, a->row_panels, a->nproj, tiles_n);
   unsigned* const heads = a->bank;                 // [kChainXcdMax] queue heads
-  unsigned* const done = a->bank + kChainXcdMax;   // finished workgroups
   unsigned* const aborted = a->bank + kChainXcdMax + 1;  // a wait of this launch expired
   unsigned* const deps = a->bank + kChainHeader;   // [nproj][row_panels]
 
@@ -583,10 +607,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
   if (!active && tid == 0)
     __hip_atomic_fetch_or(a->err, kChainErrXcc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (wave == 0) {
-    unsigned prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __builtin_amdgcn_readfirstlane(prev);
-    if (prev == gridDim.x - 1) {
+    if (chain_exit_last(a->bank, lane)) {
       // The last workgroup: every queue must have been drained (an XCD
       // without workgroups would leave its tiles undone), then the bank is
       // cleared for the next launch.
@@ -613,10 +634,23 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) + 3) / 4))) void chain_kernel
 // item's weight share first -- they depend on nothing -- and only then waits
 // until the previous projection's items are all done, so the weight of the
 // next projection streams in while the current one finishes.  Outputs and
-// activations cross XCDs here, so they move with the agent-coherent policy
-// (sc1: stores write through, loads bypass stale L2 lines), as the stream-K
-// partials do; the dependency counters are agent-scope atomics.
+// activations cross XCDs here (below: how they stay coherent); the
+// dependency counters are agent-scope atomics.
 constexpr int kPolicySc1 = 16;
+#ifndef SYS1_STREAM_FENCES
+#define SYS1_STREAM_FENCES 0
+#endif
+// Coherence across XCDs.  Default (0): every output store writes through
+// and every activation / residual load bypasses the L2 (sc1), as the
+// stream-K partials do.  1: ordinary cached accesses, with an agent-scope
+// release fence before each counter add (the XCD's L2 written back) and an
+// acquire fence after each wait (the L2 invalidated), so an activation is
+// read once per XCD rather than once per workgroup.  2: write-through stores
+// and the acquire fence only.  Measured (ModernBERT-large chain, M = 1 and
+// 64): 0 fastest, 2 +5-8%, 1 +15-30% -- the L2 write-back and invalidation
+// on every item cost more than the re-reads they save.
+constexpr int kStreamPolicy = SYS1_STREAM_FENCES ? 0 : kPolicySc1;
+constexpr int kStreamStorePolicy = SYS1_STREAM_FENCES == 1 ? 0 : kPolicySc1;
 
 template <int FM, int FN, int NW, int SMAX, int G>
 __global__ __launch_bounds__(NW * 64) void stream_chain_kernel(ChainArgs) {
@@ -625,17 +659,20 @@ __global__ __launch_bounds__(NW * 64) void stream_chain_kernel(ChainArgs) {
   constexpr int kRowF32 = BN + 4;
   static_assert(NW * BM * kRowF32 * 4 <= 160 * 1024, "LDS budget");
   static_assert(FN % 2 == 0, "whole 32-row gate/up groups per item");
+  static_assert(BM * BN / 8 <= NW * 64, "one epilogue vector per thread");
   __shared__ __attribute__((aligned(16))) float red[NW * BM * kRowF32];
-  __shared__ int slot[2];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, q = lane >> 4;
-  unsigned* const head = a->bank;
-  unsigned* const done = a->bank + kChainXcdMax;
   unsigned* const aborted = a->bank + kChainXcdMax + 1;
-  unsigned* const deps = a->bank + kChainHeader;  // items finished, per projection
+  // Items finished, per projection, counted on kStreamSlots counters (item
+  // cb on counter cb % kStreamSlots, one 128-byte line each): same-address
+  // atomics serialise, and one counter for the 164 items of a GeGLU
+  // projection cost microseconds.
+  unsigned* const deps = a->bank + kChainHeader;
+  auto dep_word = [&](int p, int s) { return deps + (p * kStreamSlots + s) * kStreamSlotStride; };
   int total = 0;
 #pragma unroll
   for (int p = 0; p < kChainMax; ++p) total += p < a->nproj ? a->proj[p].tiles_n : 0;
@@ -652,22 +689,22 @@ __global__ __launch_bounds__(NW * 64) void stream_chain_kernel(ChainArgs) {
     }
     cb = i - base;
   };
-  auto grab = [&]() -> unsigned {
-    unsigned i = 0xffffffffu;
-    if (lane == 0) i = __hip_atomic_fetch_add(head, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return i;
-  };
-  auto id_of = [&](unsigned raw) -> int {
-    const int i = (int)__builtin_amdgcn_readfirstlane(raw);
-    return i >= 0 && i < total ? i : -1;
+  // Whether every item of projection p is done: lane s reads counter s.
+  auto items_done = [&](int p) -> bool {
+    unsigned need = 0, have = 0;
+    if (lane < kStreamSlots) {
+      const int tn = a->proj[p].tiles_n;
+      need = (unsigned)(max(0, (tn - lane + kStreamSlots - 1) / kStreamSlots) + a->dep_extra);
+      have = atomic_load_agent(dep_word(p, lane));
+    }
+    return __ballot(have < need) == 0;
   };
   // Bounded wait (wave 0) for all items of projection p: as the tile chain's.
   auto wait_items = [&](int p) {
-    const unsigned need = (unsigned)(a->proj[p].tiles_n + a->dep_extra);
-    if (atomic_load_agent(deps + p) >= need || atomic_load_agent(aborted)) return;
+    if (items_done(p) || atomic_load_agent(aborted)) return;
     const uint64_t t0 = wall_clock64();
     const uint64_t budget = (uint64_t)a->wait_us * 100;
-    for (int n = 1; atomic_load_agent(deps + p) < need; ++n) {
+    for (int n = 1; !items_done(p); ++n) {
       if (wall_clock64() - t0 > budget || ((n & 15) == 0 && atomic_load_agent(aborted))) {
         if (lane == 0) {
           __hip_atomic_store(aborted, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -679,20 +716,25 @@ __global__ __launch_bounds__(NW * 64) void stream_chain_kernel(ChainArgs) {
     }
   };
 
-  if (wave == 0) {
-    const int id = id_of(grab());
-    if (lane == 0) slot[0] = id;
-  }
-  __syncthreads();
+  // Optional timeline (a->trace): per item, {id | p << 32, start, end of
+  // the dependency wait, end}, wall-clock ticks of 10 ns.
+  unsigned long long* const trace = a->trace;
+  uint64_t t_item = 0, t_dep = 0;
+  // A static schedule: workgroup b takes items b, b + grid, b + 2 grid, ...
+  // (every workgroup's items in increasing order, so the lowest unfinished
+  // item is always some workgroup's current one, and its dependencies --
+  // items of lower index -- are done: no deadlock).  With one resident
+  // workgroup per CU and ModernBERT-large's 324 items, the second round is
+  // the last projection's, taken by the workgroups of the first two.
   for (int n = 0;; ++n) {
-    const int id = __builtin_amdgcn_readfirstlane(slot[n & 1]);
-    if (id < 0) break;
+    const int64_t id64 = (int64_t)blockIdx.x + (int64_t)n * gridDim.x;
+    if (id64 >= total) break;
+    const int id = (int)id64;
+    if (trace) t_item = wall_clock64();
     int p, cb;
     decode(id, p, cb);
     const ChainProj P = proj_at(a, p);
     const int n0 = cb * BN;
-    unsigned next_raw = 0xffffffffu;
-    if (wave == 0) next_raw = grab();  // (consumed at the item's end)
 
     // ---- this wave's share of K: k-steps [s0, s1) of 32
     const int ksteps = (P.K + 31) / 32;
@@ -723,8 +765,26 @@ __global__ __launch_bounds__(NW * 64) void stream_chain_kernel(ChainArgs) {
         wreg[u][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, ok ? (int)wo[i] : (int)kOutOfRange, sw, 0);
     }
     // Then the dependency: every item of the previous projection.
-    if (p > 0 && wave == 0) wait_items(p - 1);
+    if (p > 0 && wave == 0) {
+      wait_items(p - 1);
+      if (SYS1_STREAM_FENCES) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
     __syncthreads();
+    if (trace) t_dep = wall_clock64();
+    // This thread's epilogue vector (8 output columns of one row), and its
+    // residual, loaded now beside the activations rather than after the
+    // reduction (after the wait, so a residual written by the previous
+    // projection is complete).
+    const bool gated = P.epi == kEpiGeglu || P.epi == kEpiSwiglu;
+    const int kVecs = gated ? BN / 16 : BN / 8;
+    const int out_n0 = gated ? n0 / 2 : n0;
+    const int er = tid / kVecs, ec0 = (tid % kVecs) * 8, enn = out_n0 + ec0;
+    const bool ep_ok = tid < BM * kVecs && er < a->M && enn < P.Nout;  // (Nout % 8 == 0: whole vectors)
+    i32x4 rv_raw = i32x4{0, 0, 0, 0};
+    if (P.epi == kEpiResidual && ep_ok) {
+      const rsrc_t rr = make_rsrc_uniform(P.resid, 0x7ffffff0);
+      rv_raw = __builtin_amdgcn_raw_buffer_load_b128(rr, (int)(((int64_t)er * P.ldr + enn) * 2), 0, kStreamPolicy);
+    }
     f32x4 acc[FN][FM];
 #pragma unroll
     for (int i = 0; i < FN; ++i)
@@ -741,7 +801,7 @@ __global__ __launch_bounds__(NW * 64) void stream_chain_kernel(ChainArgs) {
           const int so = __builtin_amdgcn_readfirstlane(max(0, min(st, s1 - 1)) * 64);
 #pragma unroll
           for (int j = 0; j < FM; ++j)
-            xreg[u][j] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? (int)xo[j] : (int)kOutOfRange, so, kPolicySc1);
+            xreg[u][j] = __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? (int)xo[j] : (int)kOutOfRange, so, kStreamPolicy);
         }
 #pragma unroll
         for (int u = 0; u < G; ++u)
@@ -762,16 +822,9 @@ __global__ __launch_bounds__(NW * 64) void stream_chain_kernel(ChainArgs) {
         *reinterpret_cast<f32x4*>(mine + (j * 16 + r16) * kRowF32 + i * 16 + 4 * q) = acc[i][j];
     __syncthreads();
     // Epilogue: one thread per 8 output columns of a row.
-    const bool gated = P.epi == kEpiGeglu || P.epi == kEpiSwiglu;
-    const int kVecs = gated ? BN / 16 : BN / 8;
-    const int out_n0 = gated ? n0 / 2 : n0;
     const rsrc_t yr = make_rsrc_uniform(P.y, 0x7ffffff0);
-    const rsrc_t rr = make_rsrc_uniform(P.epi == kEpiResidual ? P.resid : P.y, 0x7ffffff0);
-    for (int t = tid; t < BM * kVecs; t += NW * 64) {
-      const int r = t / kVecs, c0 = (t % kVecs) * 8;
-      if (r >= a->M) continue;
-      const int nn = out_n0 + c0;
-      if (nn >= P.Nout) continue;  // (Nout % 8 == 0: whole 16-byte vectors)
+    if (ep_ok) {
+      const int r = er, c0 = ec0, nn = enn;
       const int pc = gated ? (c0 / 16) * 32 + c0 % 16 : c0;
       float v[8], gu[8];
 #pragma unroll
@@ -804,44 +857,43 @@ __global__ __launch_bounds__(NW * 64) void stream_chain_kernel(ChainArgs) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = to_bf16(epi_gate<kEpiSwiglu>(v[e], gu[e]));
       } else if (P.epi == kEpiResidual) {
-        const bf16x8 rv = __builtin_bit_cast(
-            bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rr, (int)(((int64_t)r * P.ldr + nn) * 2), 0, kPolicySc1));
+        const bf16x8 rv = __builtin_bit_cast(bf16x8, rv_raw);
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = to_bf16(epi_apply<kEpiResidual>(v[e], 0.0f, to_f32(rv[e])));
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = to_bf16(epi_apply<kEpiNone>(v[e], 0.0f, 0.0f));
       }
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, o), yr, (int)yoff, 0, kPolicySc1);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, o), yr, (int)yoff, 0, kStreamStorePolicy);
     }
-    // The item is done once every thread's stores are: count it, publish
-    // the next item.
+    // The item is done once every thread's stores are: count it.
     vm_wait<0>();
     __syncthreads();
     if (wave == 0) {
-      const int nid = id_of(next_raw);
+      if (SYS1_STREAM_FENCES == 1) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
       if (lane == 0) {
-        __hip_atomic_fetch_add(deps + p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        slot[(n + 1) & 1] = nid;
+        __hip_atomic_fetch_add(dep_word(p, cb % kStreamSlots), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (trace && n < kChainTraceTiles) {
+          unsigned long long* r = trace + ((size_t)blockIdx.x * kChainTraceTiles + n) * 4;
+          r[0] = (unsigned long long)id | ((unsigned long long)p << 32);
+          r[1] = t_item;
+          r[2] = t_dep;
+          r[3] = wall_clock64();
+        }
       }
     }
     __syncthreads();
   }
 
-  // ---- the end: the last workgroup checks the queue and clears the bank
+  // ---- the end: the last workgroup clears the bank
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (wave == 0) {
-    unsigned prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __builtin_amdgcn_readfirstlane(prev);
-    if (prev == gridDim.x - 1) {
-      if (lane == 0 && (int)atomic_load_agent(head) < total)
-        __hip_atomic_fetch_or(a->err, kChainErrUndrained, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int words = kChainHeader + a->nproj;
-      for (int i = lane; i < words; i += 64)
-        __hip_atomic_store(a->bank + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+  if (wave == 0 && chain_exit_last(a->bank, lane)) {
+    for (int i = lane; i < kChainHeader; i += 64)
+      __hip_atomic_store(a->bank + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = lane; i < a->nproj * kStreamSlots; i += 64)
+      __hip_atomic_store(dep_word(i / kStreamSlots, i % kStreamSlots), 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

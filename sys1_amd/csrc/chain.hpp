@@ -12,6 +12,16 @@ constexpr int kChainXcdMax = 8;     // queues (one per XCD)
 constexpr int kChainHeader = 16;    // bank words before the dependency counters
 constexpr int kChainMaxPanels = 1024;  // row panels per launch (BM = 128: 131072 tokens)
 constexpr int kChainBankWords = kChainHeader + kChainMax * kChainMaxPanels;
+// The weight-streaming chain's item counters, in the dependency words: per
+// projection kStreamSlots counters, one 128-byte line each.
+constexpr int kStreamSlots = 16;
+constexpr int kStreamSlotStride = 32;
+static_assert(kChainHeader + kChainMax * kStreamSlots * kStreamSlotStride <= kChainBankWords, "bank size");
+// After the dependency words: kStreamSlots workgroup-exit counters (one
+// line each), then the error word; kChainAllocWords in all.
+constexpr int kChainExitWords = kChainBankWords;
+constexpr int kChainErrWord = kChainExitWords + kStreamSlots * kStreamSlotStride;
+constexpr int kChainAllocWords = kChainErrWord + 64;
 
 // Error word bits (sys1hip_chain_status).
 constexpr unsigned kChainErrTimeout = 1;    // a dependency wait expired

@@ -616,9 +616,9 @@ int sys1hip_init(int device, void** out) {
       hipMalloc(&c->ws, kWorkspaceBytes) != hipSuccess ||
       hipMalloc(&c->counters, kCounterSlots * sizeof(unsigned)) != hipSuccess ||
       hipMalloc(&c->stats, kNormRows * 2 * sizeof(float)) != hipSuccess ||
-      hipMalloc(&c->chain, (kChainBankWords + 64) * sizeof(unsigned)) != hipSuccess ||
+      hipMalloc(&c->chain, kChainAllocWords * sizeof(unsigned)) != hipSuccess ||
       hipMemsetAsync(c->counters, 0, kCounterSlots * sizeof(unsigned), c->own) != hipSuccess ||
-      hipMemsetAsync(c->chain, 0, (kChainBankWords + 64) * sizeof(unsigned), c->own) != hipSuccess ||
+      hipMemsetAsync(c->chain, 0, kChainAllocWords * sizeof(unsigned), c->own) != hipSuccess ||
       hipStreamSynchronize(c->own) != hipSuccess) {
     const char* msg = hipGetErrorString(hipGetLastError());
     if (c->chain) (void)hipFree(c->chain);
@@ -1273,7 +1273,7 @@ int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t
   const int occ = stream ? c->stream_chain_occ : c->chain_occ;
   if (occ < 1) return fail(SYS1HIP_EDEVICE, "%s: the chain kernel cannot be resident on this device", who);
   a.bank = c->chain;
-  a.err = c->chain + kChainBankWords;
+  a.err = c->chain + kChainErrWord;
   a.nproj = count;
   a.M = (int)M;
   a.row_panels = (int)panels;
@@ -1281,7 +1281,7 @@ int sys1hip_linear_chain_bf16(void* ctx, const sys1hip_chain_proj* proj, int32_t
   a.wait_us = c->chain_wait_us;
   a.dep_extra = c->chain_extra;
   const int grid = c->cus * occ;
-  a.trace = !stream && c->chain_trace && c->chain_trace_bytes >= (int64_t)grid * kChainTraceTiles * 32
+  a.trace = c->chain_trace && c->chain_trace_bytes >= (int64_t)grid * kChainTraceTiles * 32
                 ? c->chain_trace : nullptr;
   hipLaunchKernelGGL(reinterpret_cast<void (*)(ChainArgs)>(const_cast<void*>(ck.fn)), dim3((unsigned)grid),
                      dim3(ck.threads), 0, c->stream, a);
@@ -1314,8 +1314,8 @@ int sys1hip_chain_status(void* ctx, int32_t* flags) {
   if (rc) return rc;
   unsigned v = 0;
   HIP_TRY(hipStreamSynchronize(c->stream));
-  HIP_TRY(hipMemcpy(&v, c->chain + kChainBankWords, sizeof(v), hipMemcpyDeviceToHost));
-  if (v) HIP_TRY(hipMemset(c->chain + kChainBankWords, 0, sizeof(v)));
+  HIP_TRY(hipMemcpy(&v, c->chain + kChainErrWord, sizeof(v), hipMemcpyDeviceToHost));
+  if (v) HIP_TRY(hipMemset(c->chain + kChainErrWord, 0, sizeof(v)));
   *flags = (int32_t)v;
   return SYS1HIP_OK;
 }

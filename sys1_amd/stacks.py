@@ -141,6 +141,13 @@ CONFIGS = {
 }
 
 
+# sys1hip_linear_chain_bf16 runs a chain as a weight stream (32-column items
+# over the whole K on every CU) up to this many tokens when every K is within
+# the second bound (csrc/chain.hip: kStreamChainKernel), and as 128 x 192
+# tiles on row panels otherwise.
+STREAM_CHAIN_MAX_M = 64
+STREAM_CHAIN_MAX_K = 2688
+
 NORM_EPS = {"layer": 1e-5, "rms": 1e-6}  # ModernBERT layer_norm_eps, Qwen3.5 rms_norm_eps
 
 
