@@ -187,6 +187,7 @@ constexpr double kStoreBytesPerClk = 64.0;
 // hidden when another workgroup on the CU runs MFMAs meanwhile.
 constexpr double kTileStoreBytesPerClk = 32.0;
 constexpr double kHbmBytesPerClk = 1500.0;  // whole chip, sustained by a weight stream
+constexpr double kStreamCuFraction = 0.745;  // of the CUs, to draw the full weight-stream rate
 constexpr double kFixupClk = 2000.0;        // partial write + arrival
 constexpr double kLatencyClk = 1500.0;      // load issue -> data in LDS
 constexpr int64_t kLongK = 4096;            // see KernelEntry::long_k_efficiency
@@ -234,7 +235,15 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
       e.streamk ? share * 2.0 * e.bm * e.bn / kStoreBytesPerClk
                 : share * 2.0 * e.bm * e.bn / kTileStoreBytesPerClk * (epi == kEpiNone ? 1.0 : 2.0) *
                       (occupancy(c, id, epi) >= 2 ? 0.5 : 1.0);
-  const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk;
+  // The weight stream's floor.  Up to 128 tokens in one tile row,
+  // fewer than ~3/4 of the CUs cannot draw the chip's rate: measured on
+  // Qwen3.5-27B gate_up at M = 128 (one round of whole tiles), 182 CUs
+  // streamed 4.64 TB/s and 218 CUs 4.86 TB/s.  (Applied at M = 129-256 the
+  // same rule chose narrower tiles that ran slower: the 27B and
+  // Qwen3.5-small stacks at M = 256 lost 6-7%.)
+  const double active = (double)std::min<int64_t>(grid, c->cus);
+  const double cu_floor = M <= 128 && cdiv(M, e.bm) == 1 ? std::max(1.0, kStreamCuFraction * c->cus / active) : 1.0;
+  const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk * cu_floor;
   double t = (double)cdiv(dp, grid) * (kts * per_kt + store);
   const int64_t st = tiles - dp;
   if (st > 0) {

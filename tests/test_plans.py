@@ -37,7 +37,7 @@ E = _lib
     (256, 5248, 1024, E.EPI_GEGLU, "skinny_128x64_w4_g164"),
     (256, 1024, 2624, E.EPI_RESIDUAL, "skinny_32x32_w16_g256"),
     # Qwen3.5-27B at M = 128: weights streamed from HBM on the full stream-K grid
-    (128, 34816, 5120, E.EPI_SWIGLU, "tile_128x192_s3_w4x2_p4_g182"),
+    (128, 34816, 5120, E.EPI_SWIGLU, "tile_128x160_s3_w4x1_p4_g218"),
     (128, 5120, 17408, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
     (128, 16480, 5120, E.EPI_NONE, "stream_128x128_s4_w2x2_p4_g256"),
 ])
