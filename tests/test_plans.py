@@ -6,7 +6,7 @@ The first test pins the plans that the committed GPU measurements ran:
 - the bench line's small-M object at M = 64 and 256
   (profiles/skinny_modernbert-large_m64-m256_kernel-trace.md);
 - the Qwen3.5-27B weight stream at M = 128
-  (profiles/gemm_stream_128x128_p4_qwen35-27b-m128_kernel-trace.md).
+  (profiles/gemm_weight-stream_qwen35-27b-m128_kernel-trace.md).
 
 A change of the cost model that moves them shows here first.  The rest are
 invariants over every projection shape of the four configurations and a
