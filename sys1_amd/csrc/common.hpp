@@ -96,7 +96,8 @@ __device__ __forceinline__ float erfc_nr(float x) {
 // sequence with a correctly rounded f32 erf.
 __device__ __forceinline__ float gelu_erf(float v) {
   const float e = erfc_nr(fabsf(v) * 0.70710678118654752f);
-  const float erf = v >= 0.0f ? 1.0f - e : e - 1.0f;
+  // erf(v / sqrt 2): 1 - e for v >= 0, e - 1 = -(1 - e) (exactly) below.
+  const float erf = __builtin_copysignf(1.0f - e, v);
   return 0.5f * v * (1.0f + erf);
 }
 
@@ -137,8 +138,12 @@ __device__ __forceinline__ float epi_pre(float acc, float bias) {
 // SwiGLU follows candle's silu(gate) * up on bf16 tensors.
 template <int EPI>
 __device__ __forceinline__ float epi_gate(float g_acc, float u_acc) {
-  const float g = round_bf16(g_acc);
-  const float u = round_bf16(u_acc);
+  // both rounded to bf16 by one packed conversion
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t gu = __builtin_convertvector((f32x2_t){g_acc, u_acc}, bf16x2_t);
+  const float g = to_f32(gu[0]);
+  const float u = to_f32(gu[1]);
   float a;
   if constexpr (EPI == kEpiGeglu)
     a = round_bf16(gelu_erf(g));
