@@ -38,6 +38,9 @@ WORKLOADS = {
     "modernbert-large": ("modernbert-large", None, None, False),
     "qwen35-small": ("qwen35-small", (64, 2048), 8192, True),
     "qwen35-27b": ("qwen35-27b", (32, 1024), 4096, True),
+    # images of 64..1024 patches (multiples of the 2x2 merge do not matter
+    # to the projections) packed to 8192 patch rows
+    "qwen35-vision": ("qwen35-vision", (64, 1024), 8192, False),
 }
 
 

@@ -59,6 +59,7 @@ extern "C" {
 #define SYS1HIP_EPI_SWIGLU 4   /* y = bf16(bf16(silu(g)) * u)         qwen35_text.rs:239     */
 #define SYS1HIP_EPI_RESIDUAL 8 /* y = bf16(bf16(...) + r)             modernbert.rs:883,886  */
 #define SYS1HIP_EPI_GELU 16    /* y = bf16(gelu_erf(bf16(... + b)))   laya.rs:513-515        */
+#define SYS1HIP_EPI_GELU_TANH 64 /* y = bf16(gelu_tanh(bf16(... + b))) qwen35_vision.rs:166-169 */
 /* Not an epilogue: the weight argument is in the blocked layout of
  * sys1hip_pack_blocked_weight (ldw is then unused).  Accepted by
  * sys1hip_linear_bf16, sys1hip_linear_bf16_noalloc and

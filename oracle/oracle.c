@@ -115,6 +115,18 @@ ORC_EXPORT float orc_gelu_erf(float v) {
     return (float)(0.5 * d * (1.0 + erf(d * 0.70710678118654752440)));
 }
 
+/* gelu_tanh(v) = 0.5 v (1 + tanh(y)), y = sqrt(2/pi) (v + 0.044715 v^3), the
+ * tanh-approximate GELU that candle's `gelu` computes (the Qwen3.5 vision
+ * tower's mlp: src/archs/qwen35_vision.rs:166-169).  Evaluated in double as
+ * v / (1 + e^-2y), the same function without the cancellation of 1 + tanh(y)
+ * far left (at v = -7, 1 + tanh(y) ~ 1e-14 keeps only two digits in double),
+ * returned as f32. */
+ORC_EXPORT float orc_gelu_tanh(float v) {
+    const double d = (double)v;
+    const double y = 0.79788456080286535588 * (d + 0.044715 * d * d * d);
+    return (float)(d / (1.0 + exp(-2.0 * y)));
+}
+
 /* silu(v) = v / (1 + exp(-v)) (candle `silu`, used at src/archs/qwen35_text.rs:239). */
 ORC_EXPORT float orc_silu(float v) {
     const double d = (double)v;
@@ -288,6 +300,11 @@ ORC_EXPORT int64_t orc_pack_ragged(uint64_t seed, int64_t lo, int64_t hi, int64_
 ORC_EXPORT void orc_gelu_erf_array(const float* in, float* out, int64_t n) {
     #pragma omp parallel for schedule(static)
     for (int64_t i = 0; i < n; ++i) out[i] = orc_gelu_erf(in[i]);
+}
+
+ORC_EXPORT void orc_gelu_tanh_array(const float* in, float* out, int64_t n) {
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_gelu_tanh(in[i]);
 }
 
 ORC_EXPORT void orc_silu_array(const float* in, float* out, int64_t n) {

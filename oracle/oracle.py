@@ -59,6 +59,7 @@ def lib():
         L.orc_pack_ragged.restype = _i64
         L.orc_gelu_erf_array.argtypes = [_f32p, _f32p, _i64]
         L.orc_silu_array.argtypes = [_f32p, _f32p, _i64]
+        L.orc_gelu_tanh_array.argtypes = [_f32p, _f32p, _i64]
         L.orc_rope_tables.argtypes = [ctypes.c_double, _i64, _i64, _f32p, _f32p]
         L.orc_rope_qkv.argtypes = [_f32p, _i64, _f32p, _f32p, ctypes.POINTER(ctypes.c_int32),
                                    _i64, _i64, _i64, _f32p]
@@ -117,6 +118,15 @@ def gelu_erf(v) -> np.ndarray:
     v = _f32(v)
     out = np.empty_like(v)
     lib().orc_gelu_erf_array(_p(v), _p(out), v.size)
+    return out
+
+
+def gelu_tanh(v) -> np.ndarray:
+    """0.5 v (1 + tanh(sqrt(2/pi)(v + 0.044715 v^3))) (candle gelu, the
+    Qwen3.5 vision tower's fc1: src/archs/qwen35_vision.rs:166-169)."""
+    v = _f32(v)
+    out = np.empty_like(v)
+    lib().orc_gelu_tanh_array(_p(v), _p(out), v.size)
     return out
 
 

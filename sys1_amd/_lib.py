@@ -18,6 +18,7 @@ EPI_GEGLU = 2
 EPI_SWIGLU = 4
 EPI_RESIDUAL = 8
 EPI_GELU = 16
+EPI_GELU_TANH = 64   # bias + tanh-approximate GELU
 EPI_BLOCKED_W = 32   # not an epilogue: the weight is in the blocked layout
 GATE_GROUP = 16
 

@@ -39,7 +39,10 @@ enum Epi : int {
   // conv_ch columns, the rest plain; optionally after an RMSNorm.
   kEpiConvSilu = 12,
   kEpiNormRmsConvSilu = 13,
-  kEpiCount = 14,
+  // Bias, then the tanh-approximate GELU (the Qwen3.5 vision tower's fc1:
+  // src/archs/qwen35_vision.rs:166-169, candle's `gelu`).
+  kEpiBiasGeluTanh = 14,
+  kEpiCount = 15,
 };
 
 constexpr int kConvTaps = 4;  // DeltaNet conv kernel size (linear_conv_kernel_dim)
@@ -101,6 +104,15 @@ __device__ __forceinline__ float gelu_erf(float v) {
   return 0.5f * v * (1.0f + erf);
 }
 
+// Tanh-approximate GELU: 0.5 v (1 + tanh(y)), y = sqrt(2/pi) (v + 0.044715 v^3),
+// written as v / (1 + e^-2y) (the same function; this form keeps full
+// relative precision where 1 + tanh(y) is small), with the hardware
+// exponential and reciprocal.
+__device__ __forceinline__ float gelu_tanh(float v) {
+  const float y = 0.7978845608028654f * fmaf(0.044715f * v, v * v, v);
+  return v * __builtin_amdgcn_rcpf(1.0f + __expf(-2.0f * y));
+}
+
 // SiLU: v / (1 + e^-v) (src/archs/qwen35_text.rs:239), with the hardware
 // exponential and reciprocal (the IEEE division costs ~6% of a gated
 // projection); its bf16 results match the correctly rounded f32 sequence on
@@ -113,9 +125,10 @@ __device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcp
 template <int EPI>
 __device__ __forceinline__ float epi_apply(float acc, float bias, float resid) {
   float v = round_bf16(acc);
-  if constexpr (EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual)
+  if constexpr (EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual || EPI == kEpiBiasGeluTanh)
     v = round_bf16(v + bias);
   if constexpr (EPI == kEpiBiasGelu) v = round_bf16(gelu_erf(v));
+  if constexpr (EPI == kEpiBiasGeluTanh) v = round_bf16(gelu_tanh(v));
   if constexpr (EPI == kEpiResidual || EPI == kEpiBiasResidual) v = round_bf16(v + resid);
   return v;
 }
@@ -126,9 +139,10 @@ __device__ __forceinline__ float epi_apply(float acc, float bias, float resid) {
 template <int EPI>
 __device__ __forceinline__ float epi_pre(float acc, float bias) {
   float v = round_bf16(acc);
-  if constexpr (EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual)
+  if constexpr (EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual || EPI == kEpiBiasGeluTanh)
     v = round_bf16(v + bias);
   if constexpr (EPI == kEpiBiasGelu) v = round_bf16(gelu_erf(v));
+  if constexpr (EPI == kEpiBiasGeluTanh) v = round_bf16(gelu_tanh(v));
   return v;
 }
 
@@ -154,7 +168,7 @@ __device__ __forceinline__ float epi_gate(float g_acc, float u_acc) {
 
 template <int EPI>
 __host__ __device__ constexpr bool epi_has_bias() {
-  return EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual;
+  return EPI == kEpiBias || EPI == kEpiBiasGelu || EPI == kEpiBiasResidual || EPI == kEpiBiasGeluTanh;
 }
 template <int EPI>
 __host__ __device__ constexpr bool epi_has_resid() {

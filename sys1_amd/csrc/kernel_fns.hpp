@@ -45,7 +45,8 @@ constexpr KernelFn conv_fn() {
       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 10, PW>,                                  \
       gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 11, PW>,                                  \
       conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 12, PW>(),                                         \
-      conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 13, PW>()};                                        \
+      conv_fn<BM, BN, WM, WN, ST, BK, OCC, SK, 13, PW>(),                                         \
+      gemm_tile_kernel<BM, BN, WM, WN, ST, BK, OCC, SK, 14, PW>};                                 \
   }
 #endif
 
@@ -71,6 +72,6 @@ constexpr KernelFn skinny_fn() {
       skinny_fn<FM, FN, NW, U, 3>(),  skinny_fn<FM, FN, NW, U, 4>(),  skinny_fn<FM, FN, NW, U, 5>(),        \
       skinny_fn<FM, FN, NW, U, 6>(),  skinny_fn<FM, FN, NW, U, 7>(),  skinny_fn<FM, FN, NW, U, 8>(),        \
       skinny_fn<FM, FN, NW, U, 9>(),  skinny_fn<FM, FN, NW, U, 10>(), skinny_fn<FM, FN, NW, U, 11>(),       \
-      skinny_fn<FM, FN, NW, U, 12>(), skinny_fn<FM, FN, NW, U, 13>()};                                      \
+      skinny_fn<FM, FN, NW, U, 12>(), skinny_fn<FM, FN, NW, U, 13>(), skinny_fn<FM, FN, NW, U, 14>()};      \
   }
 #endif

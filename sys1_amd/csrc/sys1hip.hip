@@ -159,6 +159,7 @@ int epi_id_from_flags(int32_t f) {
     case SYS1HIP_EPI_SWIGLU: return kEpiSwiglu;
     case SYS1HIP_EPI_RESIDUAL: return kEpiResidual;
     case SYS1HIP_EPI_BIAS | SYS1HIP_EPI_GELU: return kEpiBiasGelu;
+    case SYS1HIP_EPI_BIAS | SYS1HIP_EPI_GELU_TANH: return kEpiBiasGeluTanh;
     case SYS1HIP_EPI_BIAS | SYS1HIP_EPI_RESIDUAL: return kEpiBiasResidual;
     default: return -1;
   }

@@ -112,20 +112,25 @@ class Linear:
         self.bias = bias
         self.out_features, self.in_features = weight.shape
 
-    def _epilogue(self, residual, gelu: bool) -> int:
+    def _epilogue(self, residual, gelu: bool | str) -> int:
+        """gelu: False, True or "erf" (exact GELU, candle's gelu_erf: Laya
+        scorer_in), or "tanh" (the tanh approximation, candle's gelu: the
+        Qwen3.5 vision tower's fc1); either needs the bias."""
         e = _lib.EPI_BLOCKED_W if self.blocked else _lib.EPI_NONE
         if self.bias is not None:
             e |= _lib.EPI_BIAS
+        if gelu not in (False, True, "erf", "tanh"):
+            raise ValueError(f"gelu must be False, True, 'erf' or 'tanh', got {gelu!r}")
         if gelu:
             if self.bias is None:
-                raise ValueError("the fused gelu epilogue needs a bias (Laya scorer_in)")
-            e |= _lib.EPI_GELU
+                raise ValueError("the fused gelu epilogues need a bias (Laya scorer_in, vision fc1)")
+            e |= _lib.EPI_GELU_TANH if gelu == "tanh" else _lib.EPI_GELU
         if residual is not None:
             e |= _lib.EPI_RESIDUAL
         return e
 
     def forward_into(self, x: torch.Tensor, out: torch.Tensor,
-                     residual: torch.Tensor | None = None, gelu: bool = False) -> torch.Tensor:
+                     residual: torch.Tensor | None = None, gelu: bool | str = False) -> torch.Tensor:
         _check_operand(x, "x", self.device)
         if x.shape[-1] != self.in_features:
             raise ValueError(f"shape mismatch: x[..., {x.shape[-1]}] vs weight "
@@ -145,7 +150,7 @@ class Linear:
         return out
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None,
-                gelu: bool = False) -> torch.Tensor:
+                gelu: bool | str = False) -> torch.Tensor:
         out = torch.empty(*x.shape[:-1], self.out_features, dtype=torch.bfloat16, device=x.device)
         return self.forward_into(x, out, residual, gelu)
 

@@ -45,6 +45,7 @@ class Proj:
     norm: str | None = None  # pre-norm of the input ("layer" / "rms"), fused when the stack has norms
     conv_ch: int = 0         # leading output columns under the DeltaNet causal conv + SiLU
     mixes_rows: bool = False  # its input comes from a row-mixing op (attention, the DeltaNet recurrence)
+    bias: bool = False        # a bias vector [nout] (epi carries EPI_BIAS)
 
     @property
     def nout(self) -> int:
@@ -56,6 +57,8 @@ class Proj:
     def bytes(self, M: int) -> int:
         """Algorithmic HBM bytes: read x and W once, write y, read residual."""
         b = 2 * (M * self.K + self.N * self.K + M * self.nout)
+        if self.bias:
+            b += 2 * self.nout
         if self.resid:
             b += 2 * M * self.nout
         return b
@@ -131,6 +134,31 @@ def qwen35(hidden: int, layers: int, heads: int, kv_heads: int, head_dim: int,
                        f"SwiGLU {H}->2x{intermediate}, down {intermediate}->{H}")
 
 
+def qwen35_vision(hidden: int, intermediate: int, depth: int, name: str) -> StackConfig:
+    """The Qwen3.5 vision tower's blocks (src/archs/qwen35_vision.rs:15-57,
+    163-171): every Linear has a bias (`dense`, :8-13); attn.qkv H->3H,
+    attn.proj H->H + residual, mlp.linear_fc1 H->I + tanh-approximate GELU
+    (candle `gelu`, :169), mlp.linear_fc2 I->H + residual.  The pre-block
+    LayerNorms (eps 1e-6) and the attention are glue outside the stack, and
+    attn.proj reads the v block as the attention output's stand-in, as the
+    text stacks do.  The merger (once per image, on merged rows) is not part
+    of the per-block stack."""
+    H, I = hidden, intermediate
+    B = _lib.EPI_BIAS
+
+    def block() -> list[Proj]:
+        return [
+            Proj("attn.qkv", H, 3 * H, B, "h", 0, "qkv", bias=True),
+            Proj("attn.proj", H, H, B | _lib.EPI_RESIDUAL, "qkv", 2 * H, "h", resid="h", mixes_rows=True,
+                 bias=True),
+            Proj("mlp.fc1+gelu_tanh", H, I, B | _lib.EPI_GELU_TANH, "h", 0, "act", bias=True),
+            Proj("mlp.fc2", I, H, B | _lib.EPI_RESIDUAL, "act", 0, "h", resid="h", bias=True),
+        ]
+    return StackConfig(name, H, [block() for _ in range(depth)],
+                       f"Qwen3.5 vision tower H={H} I={I} x{depth}: qkv {H}->{3 * H}, proj {H}->{H}, "
+                       f"fc1 {H}->{I} (bias + tanh GELU), fc2 {I}->{H}, every Linear with a bias")
+
+
 CONFIGS = {
     "modernbert-base": lambda: modernbert(768, 1152, 22, "modernbert-base"),
     "modernbert-large": lambda: modernbert(1024, 2624, 28, "modernbert-large"),
@@ -138,6 +166,11 @@ CONFIGS = {
                                    "qwen35-small"),
     "qwen35-27b": lambda: qwen35(5120, 64, 24, 4, 256, 17408, 2048, 6144, 48, 6144,
                                  "qwen35-27b"),
+    # The reference reads the vision tower's sizes from the checkpoint's
+    # config.json (VisionConfig, src/archs/qwen35_text.rs:63-75); these are
+    # the published Qwen3-VL-class tower's (hidden 1152, intermediate 4304,
+    # 27 blocks), not values the reference fixes.
+    "qwen35-vision": lambda: qwen35_vision(1152, 4304, 27, "qwen35-vision"),
 }
 
 
@@ -183,7 +216,7 @@ class ProjectionStack:
                  norms: bool = False, norm_weights: list[list[torch.Tensor | None]] | None = None,
                  norm_eps: dict[str, float] | None = None, conv: bool = False,
                  conv_weights: list[torch.Tensor | None] | None = None, blocked: bool = False,
-                 chain: bool = False):
+                 chain: bool = False, biases: list[list[torch.Tensor | None]] | None = None):
         self.cfg = cfg
         self.dev = dev
         self.max_tokens = max_tokens
@@ -196,15 +229,27 @@ class ProjectionStack:
         self.blocked = blocked
         if chain and (norms or conv):
             raise ValueError("chain=True runs projections without fused norms or conv")
+        if norms and any(p.bias and p.norm for layer in cfg.layers for p in layer):
+            raise ValueError("the fused pre-norm projections take no bias")
         self.chain = chain
         self.conv = conv
         self.conv_w: list[torch.Tensor | None] = []
         self.norm_eps = dict(NORM_EPS, **(norm_eps or {}))
         self.weights: list[list[torch.Tensor]] = []
         self.colsums: list[list[torch.Tensor | None]] = []
+        self.biases: list[list[torch.Tensor | None]] = []
         for li, layer in enumerate(cfg.layers):
-            ws, cs = [], []
+            ws, cs, bs = [], [], []
             for pi, p in enumerate(layer):
+                bvec = None
+                if p.bias:
+                    bvec = biases[li][pi] if biases is not None else None
+                    if bvec is None:
+                        bvec = torch.randn(p.nout, generator=g, device=d, dtype=torch.float32) * w_std
+                    bvec = bvec.to(device=d, dtype=torch.bfloat16).contiguous()
+                    if bvec.shape != (p.nout,):
+                        raise ValueError(f"{p.name}: bias must be [{p.nout}], got {tuple(bvec.shape)}")
+                bs.append(bvec)
                 if weights is not None:
                     w = weights[li][pi].to(device=d, dtype=torch.bfloat16).contiguous()
                 else:
@@ -224,6 +269,7 @@ class ProjectionStack:
                 cs.append(c)
             self.weights.append(ws)
             self.colsums.append(cs)
+            self.biases.append(bs)
             cwt = None
             convs = [p for p in layer if p.conv_ch]
             if conv and convs:
@@ -289,8 +335,10 @@ class ProjectionStack:
                         dst.data_ptr(), dst.stride(0), M, p.N, p.K,
                         p.epi | (_lib.EPI_BLOCKED_W if self.blocked else 0))))
                 else:
+                    bvec = self.biases[li][pi]
                     calls.append((p, self._fn, (src, ldx, w.data_ptr(), p.K if self.blocked else w.stride(0),
-                                                None, rptr, ldr, dst.data_ptr(), dst.stride(0), M, p.N, p.K,
+                                                bvec.data_ptr() if bvec is not None else None, rptr, ldr,
+                                                dst.data_ptr(), dst.stride(0), M, p.N, p.K,
                                                 p.epi | (_lib.EPI_BLOCKED_W if self.blocked else 0))))
         return calls
 

@@ -116,6 +116,9 @@ def test_every_kernel_every_epilogue(dev, orc, kid, name):
             # bias + gelu (Laya scorer_in)
             y = to_np(Linear(wg, to_gpu_bf16(bias, torch), device=dev)(xg, gelu=True))
             assert_parity(y, orc.round_bf16(orc.gelu_erf(orc.round_bf16(p16 + bb))), f"{name} bias+gelu")
+            # bias + tanh-approximate gelu (the vision tower's fc1)
+            y = to_np(Linear(wg, to_gpu_bf16(bias, torch), device=dev)(xg, gelu="tanh"))
+            assert_parity(y, orc.round_bf16(orc.gelu_tanh(orc.round_bf16(p16 + bb))), f"{name} bias+gelu_tanh")
             if not gated_ok:
                 continue
             # gated: GeGLU and SwiGLU over [2I, K] = [gate; up], I = N/2
@@ -396,6 +399,32 @@ def test_gelu_every_bf16_input(dev, orc):
     if diff.any():
         assert (np.abs(y[diff] - ref[diff]) <= bf16_ulp(ref[diff]) + 1e-30).all()
 
+
+
+def test_gelu_tanh_every_bf16_input(dev, orc):
+    """The bias + tanh-GELU epilogue over every finite bf16 value (the value
+    the activation sees is the bf16-rounded biased projection): a projection
+    with an identity weight block and a zero bias makes the output exactly
+    bf16(gelu_tanh(v)).  Against the oracle (float64, correctly rounded to
+    f32, then bf16): at most 0.1% may differ, by one bf16 ulp (the hardware
+    exponential and reciprocal)."""
+    from sys1_amd.linear import Linear
+    bits = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    v = bits[np.isfinite(bits)]
+    v = np.concatenate([v, np.zeros((-v.size) % 64, np.float32)])
+    M = v.size // 64
+    x = np.zeros((M, 64), np.float32)
+    x[:, :64] = v.reshape(M, 64)
+    w = np.eye(64, dtype=np.float32)
+    lin = Linear(to_gpu_bf16(w, torch), torch.zeros(64, dtype=torch.bfloat16, device="cuda"), device=dev)
+    print(f"[gpu] gelu_tanh over {v.size} bf16 values", flush=True)
+    y = to_np(lin(to_gpu_bf16(x, torch), gelu="tanh")).reshape(-1)
+    ref = orc.round_bf16(orc.gelu_tanh(v))
+    diff = (y != ref) & ~((y == 0) & (ref == 0)) & ~(np.isnan(y) & np.isnan(ref))
+    print(f"[gpu]   {int(diff.sum())} of {v.size} differ", flush=True)
+    assert diff.mean() <= 1e-3, f"{int(diff.sum())} of {v.size} differ"
+    if diff.any():
+        assert (np.abs(y[diff] - ref[diff]) <= bf16_ulp(ref[diff]) + 1e-30).all()
 
 def test_silu_every_bf16_input(dev, orc):
     """The SwiGLU epilogue's SiLU over every finite bf16 gate value, against

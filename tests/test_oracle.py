@@ -105,6 +105,29 @@ def test_gelu_erf_against_normal_cdf(orc):
     np.testing.assert_allclose(g, v, rtol=1e-6, atol=1e-6)
 
 
+def test_gelu_tanh_against_torch_and_closed_forms(orc):
+    """The tanh-approximate GELU (candle's gelu; the vision tower's fc1)
+    against torch's gelu(approximate="tanh") in float64, and what the formula
+    fixes: 0 at 0, the odd-part identity gelu(v) - gelu(-v) = v (tanh is
+    odd), v itself far right, and a gap of ~1e-3 to the exact GELU near 1
+    (so the erf form in its place fails)."""
+    torch = pytest.importorskip("torch")
+    v = np.linspace(-8, 8, 4001).astype(np.float32)
+    expect = torch.nn.functional.gelu(torch.from_numpy(v.astype(np.float64)), approximate="tanh").numpy()
+    np.testing.assert_allclose(orc.gelu_tanh(v), expect, rtol=2e-7, atol=1e-7)
+    # far left the oracle keeps full relative precision (torch's 1 + tanh
+    # form loses it): against v sigmoid(2y) in float64 (no cancellation)
+    vl = np.linspace(-9, -4, 501).astype(np.float32)
+    vd = vl.astype(np.float64)
+    yl = np.sqrt(2 / np.pi) * (vd + 0.044715 * vd ** 3)
+    np.testing.assert_allclose(orc.gelu_tanh(vl), vd * scipy.special.expit(2 * yl), rtol=1e-6)
+    assert orc.gelu_tanh(np.zeros(1))[0] == 0.0
+    np.testing.assert_allclose(orc.gelu_tanh(v) - orc.gelu_tanh(-v), v, rtol=1e-6, atol=1e-6)
+    assert orc.gelu_tanh(np.array([12.0]))[0] == np.float32(12.0)
+    d = abs(float(orc.gelu_tanh(np.array([1.5]))[0]) - float(orc.gelu_erf(np.array([1.5]))[0]))
+    assert 1e-4 < d < 1e-2
+
+
 def test_geglu_reference_vector(orc):
     """Reference input [2, 8] -> [2, 4]; first half is the gated (gelu) half."""
     inp = np.array(GEGLU_VALUES, np.float32).reshape(2, 8)
