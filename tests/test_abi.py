@@ -42,7 +42,7 @@ def test_version_and_kernel_table():
 
 def test_flag_values_match_header():
     text = open(HEADER).read()
-    for name in ("NONE", "BIAS", "GEGLU", "SWIGLU", "RESIDUAL", "GELU"):
+    for name in ("NONE", "BIAS", "GEGLU", "SWIGLU", "RESIDUAL", "GELU", "GELU_TANH", "BLOCKED_W"):
         m = re.search(rf"#define SYS1HIP_EPI_{name} (\d+)", text)
         assert int(m.group(1)) == getattr(_lib, f"EPI_{name}")
     for name in ("EINVAL", "EALIGN", "EDEVICE", "ERANGE"):
@@ -87,8 +87,10 @@ def _call(x=_P, ldx=64, w=_P, ldw=64, bias=None, res=None, ldr=0, y=_P, ldy=64, 
 
 @pytest.mark.parametrize("kwargs,code", [
     (dict(ctx=None), _lib.EINVAL),
-    (dict(epi=64), _lib.EINVAL),                      # unknown flag
+    (dict(epi=128), _lib.EINVAL),                     # unknown flag
     (dict(epi=_lib.EPI_GELU), _lib.EINVAL),           # gelu needs bias
+    (dict(epi=_lib.EPI_GELU_TANH), _lib.EINVAL),      # so does the tanh gelu
+    (dict(epi=_lib.EPI_GELU | _lib.EPI_GELU_TANH | _lib.EPI_BIAS), _lib.EINVAL),  # one gelu at most
     (dict(epi=_lib.EPI_GEGLU | _lib.EPI_SWIGLU), _lib.EINVAL),
     (dict(N=0), _lib.EINVAL),
     (dict(K=0), _lib.EINVAL),
