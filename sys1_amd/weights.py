@@ -16,6 +16,9 @@ blocks the projection stacks fuse into one GEMM:
                 self_attn.q_proj|k_proj|v_proj -> one, self_attn.o_proj
                 mlp.gate_proj|up_proj -> one (gate rows first), mlp.down_proj
               (src/archs/qwen35_text.rs:205-240,266-285,441-478,905-928)
+  Vision      model.visual.blocks.{i}.attn.qkv | attn.proj | mlp.linear_fc1 |
+              mlp.linear_fc2, each with its .bias
+              (src/models/clef.rs:197, src/archs/qwen35_vision.rs:8-13,37-50)
 
 Pre-norm weights (for a stack with its norms fused) by the same names:
   ModernBERT  layers.{i}.attn_norm (before Wqkv; absent in layer 0),
@@ -24,7 +27,7 @@ Pre-norm weights (for a stack with its norms fused) by the same names:
               layers.{i}.post_attention_layernorm (before gate/up)
               (src/archs/qwen35_text.rs:916-927)
 
-`read_projection_weights` / `read_norm_weights` are host-only (CPU tensors,
+`read_projection_weights` / `read_projection_biases` / `read_norm_weights` are host-only (CPU tensors,
 shapes validated against the stack); `load_stack` puts them on the device as
 a ProjectionStack (gated weights pre-packed and norm weights folded once
 there).
@@ -36,10 +39,13 @@ import os
 
 import torch
 
-from .stacks import StackConfig, modernbert, qwen35
+from .stacks import StackConfig, modernbert, qwen35, qwen35_vision
 
 MODERNBERT_PREFIX = "model."
 QWEN35_PREFIX = "model.language_model."
+VISION_PREFIX = "model.visual."  # src/models/clef.rs:197
+FAMILIES = ("modernbert", "qwen35", "qwen35_vision")
+_PREFIX = {"modernbert": MODERNBERT_PREFIX, "qwen35": QWEN35_PREFIX, "qwen35_vision": VISION_PREFIX}
 
 
 def modernbert_config(config: dict, name: str = "modernbert") -> StackConfig:
@@ -61,12 +67,28 @@ def qwen35_config(config: dict, name: str = "qwen35") -> StackConfig:
                   layer_types=c["layer_types"])
 
 
+def vision_config(config: dict, name: str = "qwen35-vision") -> StackConfig:
+    """Stack of a Qwen3.5 config.json's vision_config (hidden_size,
+    intermediate_size, depth: src/archs/qwen35_text.rs:63-75)."""
+    c = config.get("vision_config", config)
+    return qwen35_vision(c["hidden_size"], c["intermediate_size"], c["depth"], name)
+
+
+def _vision_leaf(i: int, name: str) -> str:
+    leaf = {"attn.qkv": "attn.qkv", "attn.proj": "attn.proj", "mlp.fc1+gelu_tanh": "mlp.linear_fc1",
+            "mlp.fc2": "mlp.linear_fc2"}[name]
+    return f"blocks.{i}.{leaf}"  # src/archs/qwen35_vision.rs:37-50
+
+
 def _names(family: str, cfg: StackConfig, prefix: str) -> list[list[list[str]]]:
     """Per layer, per projection of the stack: the checkpoint tensors whose
     rows it concatenates."""
     out = []
     for i, layer in enumerate(cfg.layers):
         p = f"{prefix}layers.{i}."
+        if family == "qwen35_vision":
+            out.append([[f"{prefix}{_vision_leaf(i, q.name)}.weight"] for q in layer])
+            continue
         if family == "modernbert":
             out.append([[p + "attn.Wqkv.weight"], [p + "attn.Wo.weight"], [p + "mlp.Wi.weight"],
                         [p + "mlp.Wo.weight"]])
@@ -98,11 +120,10 @@ def read_projection_weights(paths: str | list[str], family: str, cfg: StackConfi
     for a missing tensor and ValueError for a shape that does not match the
     stack."""
     from safetensors import safe_open
-    if family not in ("modernbert", "qwen35"):
+    if family not in FAMILIES:
         raise ValueError(f"unknown family {family!r}")
     paths = [paths] if isinstance(paths, (str, os.PathLike)) else list(paths)
-    prefix = prefix if prefix is not None else (MODERNBERT_PREFIX if family == "modernbert"
-                                                else QWEN35_PREFIX)
+    prefix = prefix if prefix is not None else _PREFIX[family]
     where = _index(paths)
     handles = {p: safe_open(p, framework="pt", device="cpu") for p in paths}
     weights = []
@@ -123,16 +144,47 @@ def read_projection_weights(paths: str | list[str], family: str, cfg: StackConfi
     return weights
 
 
+def read_projection_biases(paths: str | list[str], family: str, cfg: StackConfig,
+                           prefix: str | None = None) -> list[list[torch.Tensor | None]]:
+    """bf16 [nout] CPU tensors of the projections with a bias (Proj.bias;
+    the vision tower's `dense` Linears, src/archs/qwen35_vision.rs:8-13),
+    None elsewhere.  KeyError / ValueError as above."""
+    from safetensors import safe_open
+    if family not in FAMILIES:
+        raise ValueError(f"unknown family {family!r}")
+    paths = [paths] if isinstance(paths, (str, os.PathLike)) else list(paths)
+    prefix = prefix if prefix is not None else _PREFIX[family]
+    where = _index(paths)
+    handles = {p: safe_open(p, framework="pt", device="cpu") for p in paths}
+    out = []
+    for layer, names in zip(cfg.layers, _names(family, cfg, prefix)):
+        row = []
+        for proj, parts in zip(layer, names):
+            if not proj.bias:
+                row.append(None)
+                continue
+            if len(parts) != 1 or not parts[0].endswith(".weight"):
+                raise ValueError(f"{proj.name}: no single Linear to read a bias of")
+            n = parts[0][: -len("weight")] + "bias"
+            if n not in where:
+                raise KeyError(f"checkpoint has no tensor {n}")
+            b = handles[where[n]].get_tensor(n).to(torch.bfloat16)
+            if tuple(b.shape) != (proj.nout,):
+                raise ValueError(f"{n}: shape {tuple(b.shape)}, expected [{proj.nout}]")
+            row.append(b.contiguous())
+        out.append(row)
+    return out
+
+
 def read_norm_weights(paths: str | list[str], family: str, cfg: StackConfig,
                       prefix: str | None = None) -> list[list[torch.Tensor | None]]:
     """f32 [K] CPU tensors of the pre-norm of each projection with one
     (Proj.norm), None elsewhere.  KeyError / ValueError as above."""
     from safetensors import safe_open
     if family not in ("modernbert", "qwen35"):
-        raise ValueError(f"unknown family {family!r}")
+        raise ValueError(f"norm weights: unknown family {family!r} (the vision stack has no fused norms)")
     paths = [paths] if isinstance(paths, (str, os.PathLike)) else list(paths)
-    prefix = prefix if prefix is not None else (MODERNBERT_PREFIX if family == "modernbert"
-                                                else QWEN35_PREFIX)
+    prefix = prefix if prefix is not None else _PREFIX[family]
     where = _index(paths)
     handles = {p: safe_open(p, framework="pt", device="cpu") for p in paths}
     out = []
@@ -165,8 +217,12 @@ def load_stack(paths: str | list[str], family: str, config: dict | str, dev, max
     if isinstance(config, (str, os.PathLike)):
         with open(config) as f:
             config = json.load(f)
-    cfg = modernbert_config(config) if family == "modernbert" else qwen35_config(config)
+    if family not in FAMILIES:
+        raise ValueError(f"unknown family {family!r}")
+    cfg = (modernbert_config(config) if family == "modernbert" else qwen35_config(config)
+           if family == "qwen35" else vision_config(config))
     weights = read_projection_weights(paths, family, cfg, prefix)
+    biases = read_projection_biases(paths, family, cfg, prefix) if family == "qwen35_vision" else None
     nw, eps = None, None
     if norms:
         nw = read_norm_weights(paths, family, cfg, prefix)
@@ -174,4 +230,4 @@ def load_stack(paths: str | list[str], family: str, config: dict | str, dev, max
         eps = ({"layer": float(c.get("layer_norm_eps", 1e-5))} if family == "modernbert"
                else {"rms": float(c.get("rms_norm_eps", 1e-6))})
     return ProjectionStack(cfg, dev, max_tokens, weights=weights, norms=norms, norm_weights=nw,
-                           norm_eps=eps)
+                           norm_eps=eps, biases=biases)

@@ -127,3 +127,48 @@ def test_modernbert_norm_weights(tmp_path):
     st.save_file(bad, path)
     with pytest.raises(KeyError, match="attn_norm"):
         W.read_norm_weights(path, "modernbert", cfg)
+
+
+VI_CFG = {"vision_config": {"depth": 2, "hidden_size": 32, "intermediate_size": 72, "num_heads": 2,
+                            "in_channels": 3, "patch_size": 16, "temporal_patch_size": 2,
+                            "spatial_merge_size": 2, "out_hidden_size": 64,
+                            "num_position_embeddings": 64}}
+
+
+def test_vision_weights_and_biases(tmp_path):
+    """The vision tower's block Linears under model.visual.blocks.{i}
+    (src/models/clef.rs:197, src/archs/qwen35_vision.rs:37-50): weights and
+    biases in the stack's order and shapes, cast to bf16; a missing bias and
+    a wrong bias shape raise."""
+    g = torch.Generator().manual_seed(3)
+    t = {}
+    for i in range(2):
+        p = f"model.visual.blocks.{i}."
+        for leaf, (n, k) in {"attn.qkv": (96, 32), "attn.proj": (32, 32), "mlp.linear_fc1": (72, 32),
+                             "mlp.linear_fc2": (32, 72)}.items():
+            t[p + leaf + ".weight"] = _t(g, n, k)
+            t[p + leaf + ".bias"] = _t(g, n)
+        t[p + "norm1.weight"] = _t(g, 32)
+    path = str(tmp_path / "v.safetensors")
+    st.save_file(t, path)
+    cfg = W.vision_config(VI_CFG)
+    assert [p.name for p in cfg.layers[0]] == ["attn.qkv", "attn.proj", "mlp.fc1+gelu_tanh", "mlp.fc2"]
+    ws = W.read_projection_weights(path, "qwen35_vision", cfg)
+    bs = W.read_projection_biases(path, "qwen35_vision", cfg)
+    for i in range(2):
+        for q, w, b, leaf in zip(cfg.layers[i], ws[i], bs[i],
+                                 ["attn.qkv", "attn.proj", "mlp.linear_fc1", "mlp.linear_fc2"]):
+            ref = t[f"model.visual.blocks.{i}.{leaf}.weight"]
+            assert w.dtype == torch.bfloat16 and torch.equal(w, ref.to(torch.bfloat16))
+            assert torch.equal(b, t[f"model.visual.blocks.{i}.{leaf}.bias"].to(torch.bfloat16))
+            assert tuple(w.shape) == (q.N, q.K) and tuple(b.shape) == (q.nout,)
+    del t["model.visual.blocks.1.mlp.linear_fc2.bias"]
+    st.save_file(t, path)
+    with pytest.raises(KeyError, match="linear_fc2.bias"):
+        W.read_projection_biases(path, "qwen35_vision", cfg)
+    t["model.visual.blocks.1.mlp.linear_fc2.bias"] = _t(g, 33)
+    st.save_file(t, path)
+    with pytest.raises(ValueError, match="expected \\[32\\]"):
+        W.read_projection_biases(path, "qwen35_vision", cfg)
+    with pytest.raises(ValueError, match="unknown family"):
+        W.read_norm_weights(path, "qwen35_vision", cfg)
