@@ -103,3 +103,34 @@ def test_vision_stack_against_the_oracle_chain(dev, orc, M):
     print(f"[gpu]   vs bf16-rounding oracle chain {rel:.3e}; oracle chains differ by {spread:.3e}", flush=True)
     assert rel < max(4 * spread, 1e-3)
     assert_parity(out, f32, f"vision stack M={M} vs f32 chain")
+
+
+def test_vision_stack_from_safetensors_checkpoint(dev, orc, tmp_path):
+    """load_stack on a synthetic checkpoint in the reference's vision names
+    (model.visual.blocks.{i}...; src/models/clef.rs:197): the stack runs the
+    checkpoint's weights and biases, against the oracle chain of the same
+    tensors."""
+    st = pytest.importorskip("safetensors.torch")
+    from sys1_amd import weights as W
+    cfgj = {"vision_config": {"depth": 2, "hidden_size": 128, "intermediate_size": 344}}
+    cfg = W.vision_config(cfgj)
+    ws, bs = _params(orc, cfg, 900)
+    leaves = ["attn.qkv", "attn.proj", "mlp.linear_fc1", "mlp.linear_fc2"]
+    t = {}
+    for i in range(2):
+        for leaf, w, b in zip(leaves, ws[i], bs[i]):
+            t[f"model.visual.blocks.{i}.{leaf}.weight"] = torch.from_numpy(w).to(torch.bfloat16)
+            t[f"model.visual.blocks.{i}.{leaf}.bias"] = torch.from_numpy(b).to(torch.bfloat16)
+    path = str(tmp_path / "vision.safetensors")
+    st.save_file(t, path)
+    M = 777
+    print(f"[gpu] vision stack from a checkpoint M={M}", flush=True)
+    stack = W.load_stack(path, "qwen35_vision", cfgj, dev, M)
+    x = orc.fill_normal((M, 128), 5)
+    out = to_np(stack.forward(to_gpu_bf16(x, torch), M))
+    emul = _oracle_chain(orc, cfg, x, ws, bs, True)
+    f32 = _oracle_chain(orc, cfg, x, ws, bs, False)
+    rel, _ = parity(out, emul)
+    spread, _ = parity(emul, f32)
+    assert rel < max(4 * spread, 1e-3)
+    assert_parity(out, f32, "vision checkpoint stack vs f32 chain")
