@@ -134,3 +134,25 @@ def test_vision_stack_from_safetensors_checkpoint(dev, orc, tmp_path):
     spread, _ = parity(emul, f32)
     assert rel < max(4 * spread, 1e-3)
     assert_parity(out, f32, "vision checkpoint stack vs f32 chain")
+
+
+def test_vision_merger_projections(dev, orc):
+    """The tower's merger (src/archs/qwen35_vision.rs:261-268): LayerNorm,
+    2x2 patches merged into rows of 4H, linear_fc1 4H->4H with bias and the
+    exact GELU (candle gelu_erf), linear_fc2 4H->out with bias -- the bias +
+    GELU and bias epilogues on merged rows, against the oracle."""
+    from sys1_amd.linear import Linear
+    H, out_h, M = 1152, 2048, 390
+    W4 = 4 * H
+    x = orc.round_bf16(orc.fill_normal((M, W4), 61))
+    w1, b1 = orc.fill_normal((W4, W4), 62, 0.02), orc.fill_normal((W4,), 63, 0.02)
+    w2, b2 = orc.fill_normal((out_h, W4), 64, 0.02), orc.fill_normal((out_h,), 65, 0.02)
+    print(f"[gpu] vision merger M={M}", flush=True)
+    fc1 = Linear(to_gpu_bf16(w1, torch), to_gpu_bf16(b1, torch), device=dev, blocked=True)
+    fc2 = Linear(to_gpu_bf16(w2, torch), to_gpu_bf16(b2, torch), device=dev, blocked=True)
+    a = fc1(to_gpu_bf16(x, torch), gelu=True)
+    ref1 = orc.gelu_erf(orc.linear_f32(x, w1) + orc.round_bf16(b1))
+    assert_parity(to_np(a), ref1, "merger fc1 + gelu")
+    y = fc2(a)
+    assert_parity(to_np(y), orc.linear_f32(to_np(a), w2) + orc.round_bf16(b2), "merger fc2")
+    assert_parity(to_np(y), orc.linear_f32(ref1, w2) + b2, "merger chain vs f32")
