@@ -344,15 +344,20 @@ constexpr int64_t kRereadWeightBytes = 128 << 20;  // half the 256 MB MALL
 // taken (ties: the first listed), and the skinny kernels win while that
 // stays within kSkinnyCuBytes.  Measured over the ModernBERT-base/large and
 // Qwen3.5-small projections at M = 16..4096: one round at up to ~420 KB per
-// CU ran 1.1-1.9x faster than the stream-K and tile kernels, ~600 KB tied,
-// more lost; shapes needing two or more rounds lost (the Qwen3.5-small
+// CU ran 1.1-1.9x faster than the stream-K and tile kernels.  Between 576
+// and 704 KB the one-round skinny plans still won, same box (Qwen3.5 vision
+// fc2 at M = 128 on 32x32 tiles 28.6 -> 21.8 us, Qwen3.5-small down at
+// M = 64 26.3 -> 24.5, ModernBERT-large mlp.Wo at M = 1024 on 64x64 tiles
+// 27.5 -> 25.9); from 768 KB up they lost (Qwen3.5-small down at M = 128
+// 28.2 -> 31.1 us, ModernBERT-large mlp.Wo at M = 2048 36.5 -> 38.9).
+// Shapes needing two or more rounds lost (the Qwen3.5-small
 // q/k/v at M = 64 on 288 16-wide tiles: 26 against 23 us; ModernBERT-base
 // Wqkv at M = 1024 on three rounds of 64x48 tiles: 24 against 15 us).
 // Above kSkinnyWeightBytes the weight is streamed from HBM and needs the
 // stream-K schedule's spread of K over every CU.
 constexpr int64_t kSkinnyMaxM = 4096;
 constexpr int64_t kSkinnyWeightBytes = 32 << 20;
-constexpr int64_t kSkinnyCuBytes = 512 << 10;
+constexpr int64_t kSkinnyCuBytes = 704 << 10;
 
 // The skinny kernels address x and w through one buffer descriptor each,
 // based at row 0, with 32-bit byte offsets: a call whose operands span 2 GiB

@@ -6,7 +6,9 @@ The first test pins the plans that the committed GPU measurements ran:
 - the bench line's small-M object at M = 64 and 256
   (profiles/skinny_modernbert-large_m64-m256_kernel-trace.md);
 - the Qwen3.5-27B weight stream at M = 128
-  (profiles/gemm_weight-stream_qwen35-27b-m128_kernel-trace.md).
+  (profiles/gemm_weight-stream_qwen35-27b-m128_kernel-trace.md);
+- the skinny kernels' per-CU byte limit, both sides of it
+  (profiles/gemm_modernbert-large_m1024-m4096_kernel-sweep.md).
 
 A change of the cost model that moves them shows here first.  The rest are
 invariants over every projection shape of the four configurations and a
@@ -36,6 +38,13 @@ E = _lib
     (256, 1024, 1024, E.EPI_RESIDUAL, "skinny_32x32_w16_g256"),
     (256, 5248, 1024, E.EPI_GEGLU, "skinny_128x64_w4_g164"),
     (256, 1024, 2624, E.EPI_RESIDUAL, "skinny_32x32_w16_g256"),
+    # one round of skinny tiles up to 704 KB per CU (same-box A/B against the
+    # stream-K plans they replaced)
+    (1024, 1024, 2624, E.EPI_RESIDUAL, "skinny_64x64_w8_g256"),
+    (64, 2048, 6144, E.EPI_RESIDUAL, "skinny_32x16_w16_g256"),
+    (128, 1152, 4304, E.EPI_BIAS | E.EPI_RESIDUAL, "skinny_32x32_w16_g144"),
+    # ... and not beyond it
+    (128, 2048, 6144, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g80"),
     # Qwen3.5-27B at M = 128: weights streamed from HBM on the full stream-K grid
     (128, 34816, 5120, E.EPI_SWIGLU, "tile_128x160_s3_w4x1_p4_g218"),
     (128, 5120, 17408, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
