@@ -399,9 +399,23 @@ class ProjectionStack:
             if rc:
                 _lib.check(rc, self.dev.ctx)
 
-    def forward(self, x: torch.Tensor, M: int, positions: torch.Tensor | None = None) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, M: int, positions: torch.Tensor | None = None,
+                check: bool | None = None) -> torch.Tensor:
         """Enqueue the whole stack for the first M rows of x; returns the
-        hidden-state buffer (first M rows valid once the stream reaches it)."""
+        hidden-state buffer (first M rows valid once the stream reaches it).
+
+        check (default: on for a stack with chains) synchronises and reads
+        the chain launches' error word (sys1hip_chain_status): a chain whose
+        bounded dependency wait expired left invalid rows, and this raises
+        RuntimeError instead of returning them.  Callers that enqueue
+        without synchronising (run_prepared, graph capture) read it with
+        HipDevice.chain_status themselves."""
         self.dev.follow_torch_stream()
         self.run_prepared(self.prepare(x, M, positions))
+        if self.chain if check is None else check:
+            flags = self.dev.chain_status()
+            if flags:
+                raise RuntimeError(f"projection chain launch failed (sys1hip_chain_status flags {flags}: "
+                                   "1 = a dependency wait expired, 2 = a queue was not drained, "
+                                   "4 = a workgroup on an unexpected XCD); the outputs are not valid")
         return self.buffers["h"][:M, :self.cfg.hidden]

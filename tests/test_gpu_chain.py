@@ -192,8 +192,11 @@ def test_bounded_wait_expires_cleanly_and_the_next_launch_is_correct(dev, orc):
     dev.set_chain_wait(wait_us=200, extra=1 << 20)
     try:
         print("[gpu] chain with unreachable dependencies (bounded waits expire)", flush=True)
-        a.forward(x, M)
+        a.forward(x, M, check=False)
         flags = dev.chain_status()
+        # forward's own check raises on the same condition
+        with pytest.raises(RuntimeError, match="dependency wait expired"):
+            a.forward(x, M)
     finally:
         dev.set_chain_wait()
     print(f"[gpu]   status flags {flags}", flush=True)
@@ -360,8 +363,10 @@ def test_weight_streaming_chain_bounded_wait(dev, orc):
     dev.set_chain_wait(wait_us=200, extra=1 << 20)
     try:
         print("[gpu] weight-streaming chain with unreachable dependencies", flush=True)
-        a.forward(x, M)
+        a.forward(x, M, check=False)
         flags = dev.chain_status()
+        with pytest.raises(RuntimeError, match="dependency wait expired"):
+            a.forward(x, M)
     finally:
         dev.set_chain_wait()
     assert flags & 1
