@@ -121,7 +121,7 @@ struct KernelEntry {
   int wm;               // waves along M (the conv epilogue needs 1: a wave holds every row)
   int pw;               // producer waves (0: the compute waves issue the refills)
   float swiglu_efficiency;  // efficiency with a SwiGLU epilogue, when it differs (0: the same)
-  float long_k_efficiency;  // efficiency for K > kLongK, when it differs (0: the same)
+  float long_k_efficiency;  // efficiency for long K (model_cost), when it differs (0: the same)
   const KernelFn* fn;   // [kEpiCount]: the shape's kernel per epilogue (null: not built)
   bool skinny;          // skinny-M kernel (skinny.hpp): one workgroup per bm x bn tile, whole K
 };
@@ -192,6 +192,15 @@ constexpr double kStreamCuFraction = 0.745;  // of the CUs, to draw the full wei
 constexpr double kFixupClk = 2000.0;        // partial write + arrival
 constexpr double kLatencyClk = 1500.0;      // load issue -> data in LDS
 constexpr int64_t kLongK = 4096;            // see KernelEntry::long_k_efficiency
+// From K > kMidK the same rate applies once the activations no longer fit
+// one XCD's L2 (2 M K bytes above kXcdL2Bytes): the panels then stream from
+// beyond the L2 as well.  Measured on the 256x192 two-stage shape, same box:
+// Qwen3.5-small q_k_v at M = 8192 (K = 2048) 142 -> 124 us on 256x160 tiles,
+// gate_up at M = 2048 / 3072 93 -> 83 / 136 -> 123 us on 256x128 / 256x160;
+// at M = 1024 (x 4 MB, L2-resident) 256x192 stayed the faster (51.6 against
+// 55.2 us on 256x256).
+constexpr int64_t kMidK = 1536;
+constexpr int64_t kXcdL2Bytes = 4 << 20;
 // With producer waves a refill is issued as soon as its stage is freed, not
 // behind the compute waves' MFMAs: a shorter effective latency (when every
 // CU runs at least one workgroup).
@@ -219,7 +228,8 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
   const double share = (double)std::max<int64_t>(1, cdiv(grid, c->cus));
   double base_eff =
       epi_base(epi) == kEpiSwiglu && e.swiglu_efficiency > 0.0f ? e.swiglu_efficiency : e.efficiency;
-  if (K > kLongK && e.long_k_efficiency > 0.0f) base_eff = e.long_k_efficiency;
+  const bool long_k = K > kLongK || (K > kMidK && 2 * M * K > kXcdL2Bytes);
+  if (long_k && e.long_k_efficiency > 0.0f) base_eff = e.long_k_efficiency;
   const double eff = base_eff * (occupancy(c, id, epi) < e.occupancy ? kLowOccupancyRate : 1.0);
   const double mfma = 2.0 * e.bm * e.bn * e.bk / kFlopPerClk / eff;
   const double load = (double)(e.bm + e.bn) * e.bk * 2.0 / kLoadBytesPerClk;

@@ -45,6 +45,11 @@ E = _lib
     (128, 1152, 4304, E.EPI_BIAS | E.EPI_RESIDUAL, "skinny_32x32_w16_g144"),
     # ... and not beyond it
     (128, 2048, 6144, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g80"),
+    # the 256x192 two-stage shape past the L2: its long-K rate from K > 1536
+    # once x exceeds 4 MB (same-box A/B), not at M = 1024 (x L2-resident)
+    (8192, 4608, 2048, E.EPI_NONE, "tile_256x160_s3_w8x1_p4_g256"),
+    (2048, 12288, 2048, E.EPI_SWIGLU, "tile_256x128_s3_w2x2_p4_g256"),
+    (1024, 12288, 2048, E.EPI_SWIGLU, "tile_256x192_s2_w4x2_p4_g256"),
     # Qwen3.5-27B at M = 128: weights streamed from HBM on the full stream-K grid
     (128, 34816, 5120, E.EPI_SWIGLU, "tile_128x160_s3_w4x1_p4_g218"),
     (128, 5120, 17408, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
