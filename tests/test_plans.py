@@ -50,6 +50,8 @@ E = _lib
     (8192, 4608, 2048, E.EPI_NONE, "tile_256x160_s3_w8x1_p4_g256"),
     (2048, 12288, 2048, E.EPI_SWIGLU, "tile_256x128_s3_w2x2_p4_g256"),
     (1024, 12288, 2048, E.EPI_SWIGLU, "tile_256x192_s2_w4x2_p4_g256"),
+    # one round of whole 128x192 tiles over the large stream-K shapes at long K
+    (1024, 5120, 17408, E.EPI_RESIDUAL, "tile_128x192_s3_w4x2_p4_g216"),
     # Qwen3.5-27B at M = 128: weights streamed from HBM on the full stream-K grid
     (128, 34816, 5120, E.EPI_SWIGLU, "tile_128x160_s3_w4x1_p4_g218"),
     (128, 5120, 17408, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
