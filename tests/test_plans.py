@@ -8,7 +8,9 @@ The first test pins the plans that the committed GPU measurements ran:
 - the Qwen3.5-27B weight stream at M = 128
   (profiles/gemm_weight-stream_qwen35-27b-m128_kernel-trace.md);
 - the skinny kernels' per-CU byte limit, both sides of it
-  (profiles/gemm_modernbert-large_m1024-m4096_kernel-sweep.md).
+  (profiles/gemm_modernbert-large_m1024-m4096_kernel-sweep.md);
+- the plans that the forced-kernel sweeps moved
+  (profiles/gemm_all-workloads_forced-kernel-sweep.md).
 
 A change of the cost model that moves them shows here first.  The rest are
 invariants over every projection shape of the four configurations and a
@@ -50,6 +52,11 @@ E = _lib
     (8192, 4608, 2048, E.EPI_NONE, "tile_256x160_s3_w8x1_p4_g256"),
     (2048, 12288, 2048, E.EPI_SWIGLU, "tile_256x128_s3_w2x2_p4_g256"),
     (1024, 12288, 2048, E.EPI_SWIGLU, "tile_256x192_s2_w4x2_p4_g256"),
+    # the 256x192 two-stage shape priced at 0.60 (0.75 with SwiGLU) after the
+    # forced-kernel sweeps (profiles/gemm_all-workloads_forced-kernel-sweep.md)
+    (16384, 5248, 1024, E.EPI_GEGLU, "tile_256x160_s3_w8x1_p4_g256"),
+    (4096, 3072, 1024, E.EPI_NONE, "tile_128x192_s3_w4x2_p4_g256"),
+    (2048, 5248, 1024, E.EPI_GEGLU, "tile_128x192_s3_w4x2_p4_g256"),
     # one round of whole 128x192 tiles over the large stream-K shapes at long K
     (1024, 5120, 17408, E.EPI_RESIDUAL, "tile_128x192_s3_w4x2_p4_g216"),
     # Qwen3.5-27B at M = 128: weights streamed from HBM on the full stream-K grid
