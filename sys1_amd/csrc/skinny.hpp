@@ -87,6 +87,23 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // Output vectors (8 columns of one row) per thread in the epilogue below.
+  constexpr int kOutCols = kGated ? BN / 2 : BN;
+  constexpr int kVecs = kOutCols / 8;
+  const int out_n0 = kGated ? n0 / 2 : n0;
+  // When every thread has at most one output vector, its residual is
+  // loaded now, before the k-loop: it depends on nothing the kernel
+  // computes, and the epilogue then does not wait a memory round trip for
+  // it.  (The thread reads exactly the elements it later writes, so y may
+  // alias the residual.)
+  constexpr bool kResPre = epi_has_resid<E>() && !kGated && BM * kVecs <= NW * 64;
+  bf16x8 res_pre = {};
+  if constexpr (kResPre) {
+    const int t = threadIdx.x;
+    const int m = m0 + t / kVecs, n = out_n0 + (t % kVecs) * 8;
+    if (t < BM * kVecs && m < a.M && n < a.Nout) res_pre = load8_bf16(a.resid + (int64_t)m * a.ldr + n, a.Nout - n);
+  }
+
   // Two register buffers of U k-steps each: one in flight while the other
   // feeds the MFMAs.  A k-chunk at or past K (or a k-step past the wave's
   // range) reads zeros through an out-of-range offset.
@@ -140,9 +157,6 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
   // Epilogue: each thread takes 8 consecutive output columns of one row,
   // sums the waves' partials in wave order, applies the epilogue in the
   // reference's rounding order and stores 16 bytes.
-  constexpr int kOutCols = kGated ? BN / 2 : BN;
-  constexpr int kVecs = kOutCols / 8;
-  const int out_n0 = kGated ? n0 / 2 : n0;
   for (int t = threadIdx.x; t < BM * kVecs; t += NW * 64) {
     const int r = t / kVecs, c0 = (t % kVecs) * 8;
     const int m = m0 + r;
@@ -199,7 +213,12 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
     } else {
       float b[8] = {0, 0, 0, 0, 0, 0, 0, 0}, r[8] = {0, 0, 0, 0, 0, 0, 0, 0};
       if constexpr (epi_has_bias<E>()) load8(a.bias + n, b, valid);
-      if constexpr (epi_has_resid<E>()) load8(a.resid + (int64_t)m * a.ldr + n, r, valid);
+      if constexpr (kResPre) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = to_f32(res_pre[e]);
+      } else if constexpr (epi_has_resid<E>()) {
+        load8(a.resid + (int64_t)m * a.ldr + n, r, valid);
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = to_bf16(epi_apply<E>(v[e], b[e], r[e]));
     }
