@@ -11,6 +11,7 @@
  *   src/archs/qwen35_text.rs:232-240                                 (SwiGLU)
  *   src/archs/modernbert.rs:883,886; src/archs/qwen35_text.rs:938-939 (residual)
  *   src/models/laya.rs:510-520                                        (bias + gelu_erf)
+ *   src/archs/qwen35_vision.rs:163-171                                (bias + tanh GELU)
  *
  * Conventions
  *   - All tensors are device pointers (hipMalloc'd or torch-owned) in bf16,
