@@ -96,12 +96,18 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
   // computes, and the epilogue then does not wait a memory round trip for
   // it.  (The thread reads exactly the elements it later writes, so y may
   // alias the residual.)
-  constexpr bool kResPre = epi_has_resid<E>() && !kGated && BM * kVecs <= NW * 64;
-  bf16x8 res_pre = {};
-  if constexpr (kResPre) {
+  // The bias (bias epilogues) likewise.
+  constexpr bool kOnePerThread = !kGated && BM * kVecs <= NW * 64;
+  constexpr bool kResPre = epi_has_resid<E>() && kOnePerThread;
+  constexpr bool kBiasPre = epi_has_bias<E>() && kOnePerThread;
+  bf16x8 res_pre = {}, bias_pre = {};
+  if constexpr (kResPre || kBiasPre) {
     const int t = threadIdx.x;
     const int m = m0 + t / kVecs, n = out_n0 + (t % kVecs) * 8;
-    if (t < BM * kVecs && m < a.M && n < a.Nout) res_pre = load8_bf16(a.resid + (int64_t)m * a.ldr + n, a.Nout - n);
+    if (t < BM * kVecs && m < a.M && n < a.Nout) {
+      if constexpr (kResPre) res_pre = load8_bf16(a.resid + (int64_t)m * a.ldr + n, a.Nout - n);
+      if constexpr (kBiasPre) bias_pre = load8_bf16(a.bias + n, a.Nout - n);
+    }
   }
 
   // Two register buffers of U k-steps each: one in flight while the other
@@ -212,7 +218,12 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
       for (int e = 0; e < 8; ++e) o[e] = to_bf16(epi_gate<E>(v[e], g[e]));
     } else {
       float b[8] = {0, 0, 0, 0, 0, 0, 0, 0}, r[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if constexpr (epi_has_bias<E>()) load8(a.bias + n, b, valid);
+      if constexpr (kBiasPre) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) b[e] = to_f32(bias_pre[e]);
+      } else if constexpr (epi_has_bias<E>()) {
+        load8(a.bias + n, b, valid);
+      }
       if constexpr (kResPre) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) r[e] = to_f32(res_pre[e]);
