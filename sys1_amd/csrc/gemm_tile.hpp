@@ -717,9 +717,11 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
     // load behind a store to a possibly aliasing address would wait a whole
     // round trip each.  A lane reads exactly the elements it then writes, so
     // reading them all first is correct in place too.
-    // (Only for wave tiles of at most three 32x32 blocks: the larger ones
-    // have no registers to spare for the batch and would spill.)
-    constexpr bool kResRegs = epi_has_resid<E>() && !epi_gated(E) && E != kEpiRopeQkv && S::FM * S::FN <= 3;
+    // (Only for wave tiles of at most three 32x32 blocks, or four with two
+    // waves per SIMD (256 registers): the larger ones have no registers to
+    // spare for the batch and would spill.)
+    constexpr bool kResRegs = epi_has_resid<E>() && !epi_gated(E) && E != kEpiRopeQkv &&
+                              (S::FM * S::FN <= 3 || (S::FM * S::FN <= 4 && kWavesPerSimd <= 2));
     bf16x8 rres[kResRegs ? S::FM : 1][kResRegs ? S::FN : 1][2];
     if constexpr (kResRegs) {
       if (!(kResLds && res_in_lds)) {
