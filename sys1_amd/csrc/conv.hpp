@@ -2,7 +2,8 @@
 // HBM (the two-pass form of the in_proj with conv; the fused form is the
 // GEMM's conv epilogue).  Same arithmetic as that epilogue: taps over the
 // bf16 projection accumulated in f32, taps before a sequence start reading
-// zeros, SiLU with the hardware exp and reciprocal, rounded once
+// zeros, SiLU as v * (1 / (1 + e^-v)) with the hardware exp and a correctly
+// rounded division, rounded once
 // (src/archs/qwen35_text.rs:632-650; src/kernels/qwen35.cu:3-29).
 //
 // In place and parallel over rows: rows are cut into segments of S; a first

@@ -588,8 +588,9 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
   // out[r, n] = silu(sum over taps t = 3..0 of w[n, 3 - t] * p[r - t, n]),
   // p = the bf16-rounded projection, taps before the row's sequence start
   // (pos[r] < t) reading zeros; columns from conv_ch on are the plain
-  // projection (z, b, a).  The taps accumulate in f32 and the SiLU uses the
-  // hardware exp and reciprocal, rounded once to bf16: the reference rounds
+  // projection (z, b, a).  The taps accumulate in f32 and the SiLU is
+  // v * (1 / (1 + e^-v)) with the hardware exp and a correctly rounded
+  // division, rounded once to bf16: the reference rounds
   // every product and partial sum to bf16 instead, which costs three times
   // the VALU work in this epilogue and agrees to the projection tolerance.  The wave
   // holds all rows of the tile (WM = 1): row R = 32 j + lane % 32 of block
