@@ -2,8 +2,7 @@
 // HBM (the two-pass form of the in_proj with conv; the fused form is the
 // GEMM's conv epilogue).  Same arithmetic as that epilogue: taps over the
 // bf16 projection accumulated in f32, taps before a sequence start reading
-// zeros, SiLU as v * (1 / (1 + e^-v)) with the hardware exp and a correctly
-// rounded division, rounded once
+// zeros, SiLU with the hardware exp and reciprocal, rounded once
 // (src/archs/qwen35_text.rs:632-650; src/kernels/qwen35.cu:3-29).
 //
 // In place and parallel over rows: rows are cut into segments of S; a first
@@ -85,21 +84,32 @@ __global__ __launch_bounds__(256) void conv_silu_inplace_kernel(__bf16* __restri
 #pragma unroll
     for (int q = 0; q < kConvChunk; ++q) {
       const int64_t r = rc + q;
+      // A row at least kConvTaps - 1 positions into its sequence uses every
+      // tap (the common case; the row, and so the branch, is the same for
+      // the whole wave); the rows before it mask the taps that reach back
+      // past the sequence start.  Both add the same terms in the same order.
+      const bool full = ps[q] >= kConvTaps - 1;
       bf16x8 o;
 #pragma unroll
       for (int v = 0; v < kConvVec; ++v) {
         const float cur = to_f32(in[q][v]);
         float acc = 0.0f;
+        if (full) {
 #pragma unroll
-        for (int t = kConvTaps - 1; t >= 0; --t) {
-          const float xin = t == 0 ? cur : win[kConvHalo - t][v];
-          const float keep = ps[q] >= t ? 1.0f : 0.0f;
-          acc = fmaf(xin * keep, w[v][kConvTaps - 1 - t], acc);
+          for (int t = kConvTaps - 1; t >= 0; --t)
+            acc = fmaf(t == 0 ? cur : win[kConvHalo - t][v], w[v][kConvTaps - 1 - t], acc);
+        } else {
+#pragma unroll
+          for (int t = kConvTaps - 1; t >= 0; --t) {
+            const float xin = t == 0 ? cur : win[kConvHalo - t][v];
+            const float keep = ps[q] >= t ? 1.0f : 0.0f;
+            acc = fmaf(xin * keep, w[v][kConvTaps - 1 - t], acc);
+          }
         }
 #pragma unroll
         for (int h = 0; h + 1 < kConvHalo; ++h) win[h][v] = win[h + 1][v];
         win[kConvHalo - 1][v] = cur;
-        o[v] = to_bf16(acc * __frcp_rn(1.0f + __expf(-acc)));
+        o[v] = to_bf16(silu(acc));
       }
       if (r < r1) *reinterpret_cast<bf16x8*>(y + r * ldy + c) = o;
     }

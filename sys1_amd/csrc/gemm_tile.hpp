@@ -588,9 +588,9 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
   // out[r, n] = silu(sum over taps t = 3..0 of w[n, 3 - t] * p[r - t, n]),
   // p = the bf16-rounded projection, taps before the row's sequence start
   // (pos[r] < t) reading zeros; columns from conv_ch on are the plain
-  // projection (z, b, a).  The taps accumulate in f32 and the SiLU is
-  // v * (1 / (1 + e^-v)) with the hardware exp and a correctly rounded
-  // division, rounded once to bf16: the reference rounds
+  // projection (z, b, a).  The taps accumulate in f32 and the SiLU uses the
+  // hardware exp and reciprocal (as the SwiGLU epilogue), rounded once to
+  // bf16: the reference rounds
   // every product and partial sum to bf16 instead, which costs three times
   // the VALU work in this epilogue and agrees to the projection tolerance.  The wave
   // holds all rows of the tile (WM = 1): row R = 32 j + lane % 32 of block
@@ -682,7 +682,7 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const float v = val[j][e];
-              o[j][g][e] = to_bf16(v * __frcp_rn(1.0f + __expf(-v)));
+              o[j][g][e] = to_bf16(silu(v));
             }
         } else {
 #pragma unroll
