@@ -1155,14 +1155,21 @@ int sys1hip_linear_conv_silu_bf16(void* ctx, const uint16_t* x, int64_t ldx, con
   hipLaunchKernelGGL(e.fn[epi], dim3((unsigned)p.grid), dim3(e.threads), 0, c->stream, a);
   HIP_TRY(hipGetLastError());
   if (fused) return SYS1HIP_OK;
-  // Segments of S rows, one chunk (kConvChunk) each for the most threads
-  // in flight (measured: 64-row segments left the pass latency-bound at
-  // 8192 tokens), longer only when the saved halos (kConvHalo rows of
-  // conv_ch bf16 per segment) would not fit the workspace.
+  // Segments of S rows: one chunk (kConvChunk rows) each, for the most
+  // threads in flight, except from kConvLongRows rows on, where four chunks
+  // per segment still leave 2^17 threads or more (one per segment and 8
+  // channels) and save three quarters of the halo rows (3 per segment);
+  // longer only when the halos (kConvHalo rows of conv_ch bf16 per
+  // segment) would not fit the workspace.  Measured, same box: Qwen3.5-small
+  // in_proj + conv at 8192 tokens (8192 conv channels) 389.4 us at 16-row
+  // segments, 382.4 at 32, 379.0 at 64; the 27B in_proj + conv at 4096
+  // tokens 565 us at 16 rows and 568 at 32.
+  constexpr int64_t kConvLongRows = 8192;
   const int64_t vecs = conv_ch / kConvVec;
   const int64_t halo_row_bytes = (int64_t)kConvHalo * conv_ch * 2;
   const int64_t max_segs = std::max<int64_t>(1, (int64_t)kWorkspaceBytes / halo_row_bytes);
-  const int64_t S = std::max<int64_t>(kConvChunk, cdiv(cdiv(M, max_segs), kConvChunk) * kConvChunk);
+  const int64_t chunks = M >= kConvLongRows && (M / (4 * kConvChunk)) * vecs >= (1 << 17) ? 4 : 1;
+  const int64_t S = std::max<int64_t>(chunks * kConvChunk, cdiv(cdiv(M, max_segs), kConvChunk) * kConvChunk);
   const int64_t segs = cdiv(M, S);
   auto* halo = reinterpret_cast<__bf16*>(c->ws);
   if (segs > 1) {

@@ -162,6 +162,23 @@ def test_two_pass_on_a_forced_tile_kernel(dev, orc):
         dev.set_kernel(-1)
 
 
+def test_two_pass_long_segments(dev, orc):
+    """From 8192 rows with enough channels the conv pass walks 64-row
+    segments (four chunks per thread, halos only every 64 rows): sequence
+    starts on, just before and just after those boundaries."""
+    from sys1_amd import batching
+    M, C, K = 8192, 8192, 64
+    N = C + 32
+    x = orc.round_bf16(orc.fill_normal((M, K), 61))
+    w = orc.round_bf16(orc.fill_normal((N, K), 62, 0.1))
+    cw = orc.round_bf16(orc.fill_normal((C, 4), 63, 0.5))
+    cuts = sorted({0, 63, 64, 65, 127, 128, 130, 2048, 4095, 4096, 4097, 6001, 8190, M})
+    pos = batching.positions(np.diff(cuts))
+    print(f"[gpu] conv two-pass long segments M={M} N={N} C={C} K={K}", flush=True)
+    y = _run(dev, x, w, cw, None, pos, C)
+    _check(orc, dev, y, x, w, cw, None, pos, C, "long segments")
+
+
 def test_two_pass_segments_and_halos(dev, orc):
     """Rows cut into many conv segments (M well above the 64-row segment),
     sequence starts on and next to segment boundaries."""
