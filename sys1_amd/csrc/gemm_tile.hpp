@@ -740,6 +740,23 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
         }
       }
     }
+    // The bias of every column this lane stores, likewise loaded before
+    // any store (the bias does not depend on the row: FN x 2 vectors).
+    // (Only where the accumulators and the batched vectors take at most half
+    // of a wave's registers: beyond that the batch spills.)
+    constexpr bool kBiasRegs = epi_has_bias<E>() && !epi_gated(E) && E != kEpiRopeQkv &&
+                               S::FM * S::FN * 16 + S::FN * 8 + (kResRegs ? S::FM * S::FN * 8 : 0) <=
+                                   512 / kWavesPerSimd / 2;
+    bf16x8 rbias[kBiasRegs ? S::FN : 1][2];
+    if constexpr (kBiasRegs) {
+#pragma unroll
+      for (int i = 0; i < S::FN; ++i)
+#pragma unroll
+        for (int gp = 0; gp < 2; ++gp) {
+          const int n = out_n0 + i * 32 + 16 * gp + 8 * h;
+          rbias[i][gp] = n < a.Nout ? load8_bf16(a.bias + n, a.Nout - n) : bf16x8{};
+        }
+    }
 #pragma unroll
     for (int j = 0; j < S::FM; ++j) {
       const int m = m0 + wm * S::TM + j * 32 + frow;
@@ -824,7 +841,12 @@ __attribute__((amdgpu_waves_per_eu(((WM * WN + PW) * OCC + 3) / 4))) void gemm_t
               const int valid = a.Nout - n;
               if constexpr (E != kEpiNone) {
                 float b[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-                if constexpr (epi_has_bias<E>()) load8(a.bias + n, b, valid);
+                if constexpr (kBiasRegs) {
+#pragma unroll
+                  for (int e = 0; e < 8; ++e) b[e] = to_f32(rbias[i][gp][e]);
+                } else if constexpr (epi_has_bias<E>()) {
+                  load8(a.bias + n, b, valid);
+                }
                 float r[8];
                 if constexpr (epi_has_resid<E>()) {
                   if (kResLds && res_in_lds) {
