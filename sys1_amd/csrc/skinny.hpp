@@ -109,6 +109,30 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
       if constexpr (kBiasPre) bias_pre = load8_bf16(a.bias + n, a.Nout - n);
     }
   }
+  // The pre-norm epilogues' row statistics and column sums (written by
+  // the statistics pass before this launch), likewise.
+  constexpr bool kNormPre = NORM != kNormNone && kOnePerThread;
+  float rs_pre = 0.0f, mu_pre = 0.0f, cs_pre[kNormPre && NORM == kNormLayer ? 8 : 1] = {};
+  if constexpr (kNormPre) {
+    const int t = threadIdx.x;
+    const int m = min(m0 + t / kVecs, a.M - 1), c0 = (t % kVecs) * 8;
+    rs_pre = a.stats[2 * (int64_t)m + 1];
+    if constexpr (NORM == kNormLayer) {
+      mu_pre = a.stats[2 * (int64_t)m];
+      if (n0 + c0 + 8 <= a.N) {  // two 16-byte reads (kNormPre implies not gated)
+        const f32x4 c0v = *reinterpret_cast<const f32x4*>(a.colsum + n0 + c0);
+        const f32x4 c1v = *reinterpret_cast<const f32x4*>(a.colsum + n0 + c0 + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          cs_pre[e] = c0v[e];
+          cs_pre[4 + e] = c1v[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cs_pre[e] = a.colsum[min(n0 + c0 + e, a.N - 1)];
+      }
+    }
+  }
 
   // Two register buffers of U k-steps each: one in flight while the other
   // feeds the MFMAs.  A k-chunk at or past K (or a k-step past the wave's
@@ -198,13 +222,14 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs a) {
     }
     // (for gated epilogues v holds the gate sums and g the up sums)
     if constexpr (NORM != kNormNone) {
-      const float r = a.stats[2 * (int64_t)m + 1];
-      const float mu = NORM == kNormLayer ? a.stats[2 * (int64_t)m] : 0.0f;
+      const float r = kNormPre ? rs_pre : a.stats[2 * (int64_t)m + 1];
+      const float mu = NORM == kNormLayer ? (kNormPre ? mu_pre : a.stats[2 * (int64_t)m]) : 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if constexpr (NORM == kNormLayer) {
           const int wn = min(n0 + pc + e, a.N - 1);  // weight row of the gate (or plain) column
-          v[e] = r * (v[e] - mu * a.colsum[wn]);
+          const float cs = kNormPre ? cs_pre[e] : a.colsum[wn];
+          v[e] = r * (v[e] - mu * cs);
           if constexpr (kGated) g[e] = r * (g[e] - mu * a.colsum[min(wn + 16, a.N - 1)]);
         } else {
           v[e] *= r;
