@@ -189,6 +189,8 @@ constexpr double kStoreBytesPerClk = 64.0;
 constexpr double kTileStoreBytesPerClk = 32.0;
 constexpr double kHbmBytesPerClk = 1500.0;  // whole chip, sustained by a weight stream
 constexpr double kStreamCuFraction = 0.745;  // of the CUs, to draw the full weight-stream rate
+constexpr int64_t kCachedWeightBytes = 32 << 20;  // weights up to this size stay in the caches
+constexpr double kRereadShare = 0.25;  // of a streamed weight's re-walks charged at the HBM rate
 constexpr double kFixupClk = 2000.0;        // partial write + arrival
 constexpr double kLatencyClk = 1500.0;      // load issue -> data in LDS
 constexpr int64_t kLongK = 4096;            // see KernelEntry::long_k_efficiency
@@ -254,7 +256,13 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
   // Qwen3.5-small stacks at M = 256 lost 6-7%.)
   const double active = (double)std::min<int64_t>(grid, c->cus);
   const double cu_floor = M <= 128 && cdiv(M, e.bm) == 1 ? std::max(1.0, kStreamCuFraction * c->cus / active) : 1.0;
-  const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk * cu_floor;
+  // A stream-K weight beyond the caches is walked once per row panel, and
+  // part of each walk after the first comes from HBM again: measured on
+  // the 27B out_proj (63 MB) at M = 272, 102.8 us on nine 32-row panels
+  // against 60.9 us on three 128-row panels, same box.
+  const double rereads =
+      e.streamk && 2 * N * K > kCachedWeightBytes ? 1.0 + kRereadShare * (double)(cdiv(M, e.bm) - 1) : 1.0;
+  const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk * cu_floor * rereads;
   double t = (double)cdiv(dp, grid) * (kts * per_kt + store);
   const int64_t st = tiles - dp;
   if (st > 0) {
@@ -343,7 +351,6 @@ int64_t halo_rows(const KernelEntry& e, int64_t M, int halo) {
 
 // conv: only shapes with a conv epilogue (waves spanning every row), priced
 // on the rows their overlapping tile rows compute.
-constexpr int64_t kCachedWeightBytes = 32 << 20;
 constexpr int64_t kRereadWeightBytes = 128 << 20;  // half the 256 MB MALL
 
 // The skinny-M kernel for a call, or -1.  A skinny workgroup reads its BN

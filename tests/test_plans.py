@@ -63,6 +63,12 @@ E = _lib
     (128, 34816, 5120, E.EPI_SWIGLU, "tile_128x160_s3_w4x1_p4_g218"),
     (128, 5120, 17408, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
     (128, 16480, 5120, E.EPI_NONE, "stream_128x128_s4_w2x2_p4_g256"),
+    # a 63 MB weight over several row panels: 128-row stream-K panels, not
+    # nine 32-row ones that walk the weight nine times (out_proj / o_proj)
+    (272, 5120, 6144, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
+    (288, 5120, 6144, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
+    # small weights stay in the caches: 32-row panels remain the pick
+    (256, 2048, 6144, E.EPI_RESIDUAL, "stream_32x256_s4_w1x4_p4_g256"),
 ])
 def test_plans_of_the_measured_workloads(M, N, K, epi, plan):
     kid, grid, name = _lib.plan_kernel(M, N, K, epi)
