@@ -191,6 +191,8 @@ constexpr double kHbmBytesPerClk = 1500.0;  // whole chip, sustained by a weight
 constexpr double kStreamCuFraction = 0.745;  // of the CUs, to draw the full weight-stream rate
 constexpr int64_t kCachedWeightBytes = 32 << 20;  // weights up to this size stay in the caches
 constexpr double kRereadShare = 0.25;  // of a streamed weight's re-walks charged at the HBM rate
+constexpr double kRereadShareBig = 0.5;  // the same, for weights beyond half the MALL
+constexpr int64_t kRereadWeightBytes = 128 << 20;  // half the 256 MB MALL
 constexpr double kFixupClk = 2000.0;        // partial write + arrival
 constexpr double kLatencyClk = 1500.0;      // load issue -> data in LDS
 constexpr int64_t kLongK = 4096;            // see KernelEntry::long_k_efficiency
@@ -259,9 +261,13 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
   // A stream-K weight beyond the caches is walked once per row panel, and
   // part of each walk after the first comes from HBM again: measured on
   // the 27B out_proj (63 MB) at M = 272, 102.8 us on nine 32-row panels
-  // against 60.9 us on three 128-row panels, same box.
+  // against 60.9 us on three 128-row panels.  Beyond half the MALL the
+  // share is larger: the 27B down (178 MB) at M = 512 / 768 ran 145.7 /
+  // 211.8 us on 128-row panels against 112.8 / 155.9 on 256-row ones
+  // (~17 us per extra walk, against ~1 us for out_proj at M = 512).
+  const double reread_share = 2 * N * K > kRereadWeightBytes ? kRereadShareBig : kRereadShare;
   const double rereads =
-      e.streamk && 2 * N * K > kCachedWeightBytes ? 1.0 + kRereadShare * (double)(cdiv(M, e.bm) - 1) : 1.0;
+      e.streamk && 2 * N * K > kCachedWeightBytes ? 1.0 + reread_share * (double)(cdiv(M, e.bm) - 1) : 1.0;
   const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk * cu_floor * rereads;
   double t = (double)cdiv(dp, grid) * (kts * per_kt + store);
   const int64_t st = tiles - dp;
@@ -351,7 +357,6 @@ int64_t halo_rows(const KernelEntry& e, int64_t M, int halo) {
 
 // conv: only shapes with a conv epilogue (waves spanning every row), priced
 // on the rows their overlapping tile rows compute.
-constexpr int64_t kRereadWeightBytes = 128 << 20;  // half the 256 MB MALL
 
 // The skinny-M kernel for a call, or -1.  A skinny workgroup reads its BN
 // weight rows and its BM rows of x over the whole K, and one round of

@@ -67,6 +67,11 @@ E = _lib
     # nine 32-row ones that walk the weight nine times (out_proj / o_proj)
     (272, 5120, 6144, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
     (288, 5120, 6144, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
+    # a 178 MB weight (beyond half the MALL): 256-row panels walk it half as
+    # often as 128-row ones (down); the 63 MB out_proj keeps 128-row panels
+    (512, 5120, 17408, E.EPI_RESIDUAL, "stream_256x128_s3_w4x2_g256"),
+    (768, 5120, 17408, E.EPI_RESIDUAL, "stream_256x128_s3_w4x2_g256"),
+    (512, 5120, 6144, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
     # small weights stay in the caches: 32-row panels remain the pick
     (256, 2048, 6144, E.EPI_RESIDUAL, "stream_32x256_s4_w1x4_p4_g256"),
 ])
