@@ -72,6 +72,10 @@ E = _lib
     (512, 5120, 17408, E.EPI_RESIDUAL, "stream_256x128_s3_w4x2_g256"),
     (768, 5120, 17408, E.EPI_RESIDUAL, "stream_256x128_s3_w4x2_g256"),
     (512, 5120, 6144, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
+    # SwiGLU at 272-896 tokens: not 128x128 tiles at two per CU
+    (384, 34816, 5120, E.EPI_SWIGLU, "tile_256x160_s3_w8x1_p4_g256"),
+    (640, 34816, 5120, E.EPI_SWIGLU, "tile_256x160_s3_w8x1_p4_g256"),
+    (896, 34816, 5120, E.EPI_SWIGLU, "tile_128x192_s3_w4x2_p4_g256"),
     # small weights stay in the caches: 32-row panels remain the pick
     (256, 2048, 6144, E.EPI_RESIDUAL, "stream_32x256_s4_w1x4_p4_g256"),
 ])
