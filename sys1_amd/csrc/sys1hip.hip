@@ -192,6 +192,7 @@ constexpr double kStreamCuFraction = 0.745;  // of the CUs, to draw the full wei
 constexpr int64_t kCachedWeightBytes = 32 << 20;  // weights up to this size stay in the caches
 constexpr double kRereadShare = 0.25;  // of a streamed weight's re-walks charged at the HBM rate
 constexpr double kRereadShareBig = 0.5;  // the same, for weights beyond half the MALL
+constexpr double kRereadShareCached = 0.3;  // the same, in clocks of that rate, for weights the caches hold
 constexpr int64_t kRereadWeightBytes = 128 << 20;  // half the 256 MB MALL
 constexpr double kFixupClk = 2000.0;        // partial write + arrival
 constexpr double kLatencyClk = 1500.0;      // load issue -> data in LDS
@@ -264,10 +265,15 @@ double model_cost(const Context* c, int id, int epi, int64_t M, int64_t N, int64
   // against 60.9 us on three 128-row panels.  Beyond half the MALL the
   // share is larger: the 27B down (178 MB) at M = 512 / 768 ran 145.7 /
   // 211.8 us on 128-row panels against 112.8 / 155.9 on 256-row ones
-  // (~17 us per extra walk, against ~1 us for out_proj at M = 512).
-  const double reread_share = 2 * N * K > kRereadWeightBytes ? kRereadShareBig : kRereadShare;
-  const double rereads =
-      e.streamk && 2 * N * K > kCachedWeightBytes ? 1.0 + reread_share * (double)(cdiv(M, e.bm) - 1) : 1.0;
+  // (~17 us per extra walk, against ~1 us for out_proj at M = 512).  A
+  // weight the caches hold still pays for its walks in clocks: the
+  // Qwen3.5-small out_proj (16 MB) at M = 960 ran 65.9 us on thirty 32-row
+  // panels against 38.5 us on eight 128-row ones, its down (24 MB) at
+  // M = 576 59.0 against 40.1 us.
+  const double reread_share = 2 * N * K > kRereadWeightBytes   ? kRereadShareBig
+                              : 2 * N * K > kCachedWeightBytes ? kRereadShare
+                                                               : kRereadShareCached;
+  const double rereads = e.streamk ? 1.0 + reread_share * (double)(cdiv(M, e.bm) - 1) : 1.0;
   const double hbm = 2.0 * (double)N * K / kHbmBytesPerClk * cu_floor * rereads;
   double t = (double)cdiv(dp, grid) * (kts * per_kt + store);
   const int64_t st = tiles - dp;

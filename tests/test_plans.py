@@ -76,8 +76,11 @@ E = _lib
     (384, 34816, 5120, E.EPI_SWIGLU, "tile_256x160_s3_w8x1_p4_g256"),
     (640, 34816, 5120, E.EPI_SWIGLU, "tile_256x160_s3_w8x1_p4_g256"),
     (896, 34816, 5120, E.EPI_SWIGLU, "tile_128x192_s3_w4x2_p4_g256"),
-    # small weights stay in the caches: 32-row panels remain the pick
+    # small weights stay in the caches: 32-row panels remain the pick at a
+    # few panels, 128-row ones take over as the walks add up
     (256, 2048, 6144, E.EPI_RESIDUAL, "stream_32x256_s4_w1x4_p4_g256"),
+    (576, 2048, 6144, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
+    (960, 2048, 4096, E.EPI_RESIDUAL, "stream_128x128_s4_w2x2_p4_g256"),
 ])
 def test_plans_of_the_measured_workloads(M, N, K, epi, plan):
     kid, grid, name = _lib.plan_kernel(M, N, K, epi)
